@@ -1,0 +1,260 @@
+"""Benchmark of the MI355X packed 4-bit affine quantized matmul (one GPU).
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--only c0,c1,...] [--no-cpu]
+
+Headline (the JSON `value`): the decode gate+up workload — x bf16 [M, 5120] for M = 1, 2 and 4
+batched requests against packed 4-bit weights [34816, 5120] (group 64). One step = the three
+quantized matmuls (M = 1, 2, 4), each on its own copy of the weights; copies rotate so the
+256 MB Infinity Cache cannot serve them (>= 640 MB of distinct weights). value = algorithmic
+bytes of the K timed steps / their GPU time (HIP events around the whole region), in GB/s.
+
+Also measured (the `workloads` object): every benchmark workload's kernel time per call (median
+of >= 20 single-launch HIP-event samples on rotating weight copies), achieved HBM GB/s and MFMA
+TFLOP/s against MI355X peaks (8 TB/s; 2.5 PFLOP/s dense bf16). The `roofline` object is the
+dominant kernel of the headline: algorithmic bytes per launch / mean launch duration, measured
+with per-launch HIP events on the launch stream in a second pass of K steps.
+
+cpu_baseline: the oracle's C restatement (OpenMP, fp32 accumulation) on the host cores, on a
+bounded, time-boxed sample of the same decode steps.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+
+import numpy as np
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, os.path.join(ROOT, "mlx-tree-spec_amd"))
+
+METRIC = "qmm µs + HBM GB/s (% of peak) at M=1–64; TFLOP/s at M=4096 prefill"
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+MALL_BYTES = 256 << 20
+ROTATE_BYTES = 640e6
+
+WORKLOADS = {
+    # name: (config index, rows, K, N, sigma)
+    "c0": (0, (16,), 5120, 5120, 1.0),
+    "c1": (1, (1, 2, 4), 5120, 34816, 1.0),
+    "c2": (2, (64,), 17408, 5120, 0.5),
+    "c3": (3, (32,), 5120, 151936, 1.0),
+    "c4": (4, (4096,), 5120, 17408, 1.0),
+}
+DESCR = {
+    "c0": "tree-verify qmm: x bf16 [16, 5120] @ packed 4-bit [5120, 5120]",
+    "c1": "decode gate+up: x bf16 [M=1,2,4, 5120] @ packed 4-bit [34816, 5120]",
+    "c2": "batched verify down proj: x bf16 [64, 17408] @ packed 4-bit [5120, 17408]",
+    "c3": "vocab head: x bf16 [32, 5120] @ packed 4-bit [151936, 5120]",
+    "c4": "chunked prefill: x bf16 [4096, 5120] @ packed 4-bit [17408, 5120]",
+}
+
+
+def log(msg: str) -> None:
+    print(msg, file=sys.stderr, flush=True)
+
+
+def bytes_per_call(m: int, k: int, n: int) -> int:
+    return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * m * k + 2 * m * n
+
+
+class Workload:
+    """Device-resident inputs of one benchmark workload with rotating weight copies."""
+
+    def __init__(self, name: str, torch, lib, dev):
+        from oracle import qmm4_oracle as O  # synthetic-input generator only
+
+        idx, rows, k, n, sigma = WORKLOADS[name]
+        self.name, self.rows, self.k, self.n = name, rows, k, n
+        x, w, s, b = O.make_inputs(max(rows), k, n, sigma=sigma, seed=idx)
+        wbytes = n * k // 2 + 4 * n * (k // 64)
+        self.copies = max(2, int(np.ceil(ROTATE_BYTES / wbytes)))
+        t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(dev)
+        w0, s0, b0 = t(w, np.int32), t(s, np.int16), t(b, np.int16)
+        self.w = [w0] + [w0.clone() for _ in range(self.copies - 1)]
+        self.s = [s0] + [s0.clone() for _ in range(self.copies - 1)]
+        self.b = [b0] + [b0.clone() for _ in range(self.copies - 1)]
+        self.x = t(x, np.int16)
+        self.y = {m: torch.empty((m, n), dtype=torch.int16, device=dev) for m in rows}
+        self.lib = lib
+        self.stream = torch.cuda.current_stream(dev).cuda_stream
+        self.i = 0
+
+    def launch(self, m: int, copy: int | None = None) -> None:
+        c = self.i % self.copies if copy is None else copy
+        self.i += 1
+        rc = self.lib.qmm4_affine_bf16(self.x.data_ptr(), self.w[c].data_ptr(), self.s[c].data_ptr(),
+                                       self.b[c].data_ptr(), self.y[m].data_ptr(), m, self.n, self.k, 64, 4, 1,
+                                       self.stream)
+        if rc != 0:
+            raise RuntimeError(f"qmm4_affine_bf16 failed ({rc}): {self.lib.qmm4_last_error().decode()}")
+
+    def step(self) -> None:
+        for m in self.rows:
+            self.launch(m)
+
+    def step_bytes(self) -> int:
+        return sum(bytes_per_call(m, self.k, self.n) for m in self.rows)
+
+
+def time_launches(torch, wl: Workload, m: int, samples: int) -> list[float]:
+    """Per-launch kernel time (s) from HIP event pairs on the launch stream."""
+    evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
+    for a, b in evs:
+        a.record()
+        wl.launch(m)
+        b.record()
+    torch.cuda.synchronize()
+    return [a.elapsed_time(b) * 1e-3 for a, b in evs]
+
+
+def cpu_baseline(wl_rows, k, n, budget_s: float = 10.0) -> dict:
+    from oracle import cpu
+    from oracle import qmm4_oracle as O
+
+    x, w, s, b = O.make_inputs(max(wl_rows), k, n, seed=1)
+    threads = cpu.num_threads()
+    cpu.qmm(x[:1], w, s, b)  # warm-up
+    t0 = time.perf_counter()
+    steps = 0
+    while True:
+        for m in wl_rows:
+            cpu.qmm(x[:m], w, s, b)
+        steps += 1
+        el = time.perf_counter() - t0
+        if el >= budget_s or steps >= 200:
+            break
+    total = steps * sum(bytes_per_call(m, k, n) for m in wl_rows)
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
+    except OSError:
+        pass
+    return {"value": round(total / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
+            "sample": f"{steps} decode steps (M=1,2,4 x 5120 -> 34816) in {el:.1f} s, {threads} OpenMP threads, "
+                      f"oracle/qmm4_cpu.c (fp32 accumulation), CPU: {model}",
+            "ms_per_step": round(el / steps * 1e3, 2)}
+
+
+def main() -> int:
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=200)
+    ap.add_argument("--warmup", type=int, default=20)
+    ap.add_argument("--only", default="c0,c1,c2,c3,c4", help="workloads to measure (c1 is the headline)")
+    ap.add_argument("--samples", type=int, default=30, help="single-launch samples per workload")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    args = ap.parse_args()
+
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        log("bench.py measures one GPU: this build has no multi-GPU path (the kernel is per-GPU; "
+            "sharding over output columns is described in DESIGN.md). Run with --gpus 1.")
+        return 2
+
+    import torch
+
+    from mlx_tree_spec_amd import _lib
+
+    if not torch.cuda.is_available():
+        log("no HIP device visible")
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = _lib.load()
+    only = [s.strip() for s in args.only.split(",") if s.strip()]
+    if "c1" not in only:
+        only = ["c1"] + only
+
+    out_workloads = {}
+    head = None
+    for name in only:
+        log(f"[bench] {name}: {DESCR[name]}")
+        wl = Workload(name, torch, lib, dev)
+        for _ in range(3):
+            wl.step()
+        torch.cuda.synchronize()
+        res = {"descr": DESCR[name], "weight_copies": wl.copies, "per_m": {}}
+        for m in wl.rows:
+            ts = time_launches(torch, wl, m, args.samples)
+            med = statistics.median(ts)
+            byt = bytes_per_call(m, wl.k, wl.n)
+            fl = 2 * m * wl.n * wl.k
+            res["per_m"][str(m)] = {
+                "us": round(med * 1e6, 2), "gbs": round(byt / med / 1e9, 1),
+                "hbm_frac": round(byt / med / 1e9 / HBM_PEAK_GBS, 4),
+                "tflops": round(fl / med / 1e12, 2), "mfma_frac": round(fl / med / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+                "bytes": byt, "flops": fl, "samples": len(ts)}
+            log(f"[bench]   M={m}: {med * 1e6:8.2f} us  {byt / med / 1e9:7.1f} GB/s  {fl / med / 1e12:7.1f} TFLOP/s")
+        out_workloads[name] = res
+        if name == "c1":
+            head = (wl, res)
+        else:
+            del wl
+            torch.cuda.empty_cache()
+
+    wl, res = head
+    # Timed region: exactly K steps, synchronized on both sides.
+    for _ in range(args.warmup):
+        wl.step()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(args.steps):
+        wl.step()
+    end.record()
+    torch.cuda.synchronize()
+    total_s = start.elapsed_time(end) * 1e-3
+    value = wl.step_bytes() * args.steps / total_s / 1e9
+
+    # Second pass: per-launch durations of the dominant kernel (same steps, events per launch).
+    durs, byts = [], []
+    evs = []
+    for _ in range(args.steps):
+        for m in wl.rows:
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            wl.launch(m)
+            b.record()
+            evs.append((a, b, m))
+    torch.cuda.synchronize()
+    for a, b, m in evs:
+        durs.append(a.elapsed_time(b) * 1e-3)
+        byts.append(bytes_per_call(m, wl.k, wl.n))
+    achieved = sum(byts) / sum(durs) / 1e9
+    traffic = None
+    tpath = os.path.join(ROOT, "profiles", "traffic_decode_gate_up.json")
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            traffic = json.load(f).get("hbm_bytes_per_launch")
+
+    line = {
+        "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(total_s / args.steps * 1e3, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
+        "config": {"workload": "decode gate+up projection: x bf16 [M, 5120] for M = 1, 2, 4 batched requests @ "
+                               "packed 4-bit affine [34816, 5120] (group 64, bf16 scales/biases), bf16 out; one step "
+                               "= the three calls", "M": [1, 2, 4], "K": 5120, "N": 34816, "group_size": 64,
+                   "weight_copies": wl.copies},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "qmm4::skinny_kernel (M<=16 variant)",
+                     "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
+                     "bytes_per_launch": round(statistics.mean(byts))},
+        "workloads": out_workloads,
+    }
+    if not args.no_cpu:
+        log("[bench] cpu baseline")
+        line["cpu_baseline"] = cpu_baseline(wl.rows, wl.k, wl.n, args.cpu_seconds)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

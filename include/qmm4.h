@@ -1,0 +1,70 @@
+/*
+ * qmm4.h — C ABI of the MI355X (gfx950) packed 4-bit affine quantized matmul.
+ *
+ * Format (MLX affine, 4 bits, group 64; the layout of mlx.nn.QuantizedLinear as used by
+ * src/mlx_tree_spec/packed_linear.py:49-58 and read by src/mlx_tree_spec/qmm_packed.py):
+ *   w       uint32 [N, K/8]   code q[n, 8c+i] = (w[n, c] >> 4i) & 0xF        (qmm_packed.py:115, 200-201)
+ *   scales  bf16   [N, K/64]  s[n, g],  g = k / 64                           (qmm_packed.py:454, 630)
+ *   biases  bf16   [N, K/64]  b[n, g]
+ *   dequant w_deq[n, k] = bf16_rne(fp32(s) * q + fp32(b))                   (qmm_packed.py:635-636)
+ *   y[m, n] = bf16_rne(sum_k fp32(x[m, k]) * fp32(w_deq[n, k]))  (fp32 accumulation, any order)
+ *
+ * Conventions for every entry point:
+ *   - all array pointers are caller-owned HIP device pointers on the current device, row-major and
+ *     contiguous; bf16 arrays are passed as raw 16-bit words (void*), so no host type is implied;
+ *   - work is enqueued asynchronously on `hip_stream` (a hipStream_t; NULL = the default stream);
+ *   - return 0 on success or a negative QMM4_ERR_* code; qmm4_last_error() then returns a
+ *     message for the calling host thread;
+ *   - the library keeps one internal workspace per (device, stream) for split-K partial sums;
+ *     calls on the same stream are ordered, calls on different streams use different workspaces.
+ */
+#ifndef MI355X_QMM4_H
+#define MI355X_QMM4_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define QMM4_OK 0
+#define QMM4_ERR_INVALID (-22)     /* bad shape, null pointer, misaligned pointer       */
+#define QMM4_ERR_UNSUPPORTED (-95) /* bits != 4, group_size != 64, transpose == 0       */
+#define QMM4_ERR_NOMEM (-12)       /* workspace allocation failed                       */
+#define QMM4_ERR_HIP (-5)          /* a HIP runtime call failed (message has the name)  */
+
+/*
+ * y = x @ dequant(w)^T  — the quantized-matmul call of the verify, decode and prefill passes.
+ * Replaces mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4) as
+ * called at src/mlx_tree_spec/packed_linear.py:97, and the packed kernels behind
+ * packed_linear._call (packed_linear.py:83-104; qmm_packed.py:270-293, 372-394, 529-551, 701-725).
+ *   x: bf16 [M, K]; w: uint32 [N, K/8]; scales, biases: bf16 [N, K/group_size]; y: bf16 [M, N].
+ *   Requires M >= 0, N % 16 == 0, K % 128 == 0 (the reference's packed path requires K % 128 == 0,
+ *   packed_linear.py:57), group_size == 64, bits == 4, transpose == 1, 16-byte aligned x and w.
+ *   M == 0 or N == 0 is a no-op. Rows M <= 64 run the skinny HBM-bound kernel, larger M the
+ *   MFMA GEMM; the choice is a fixed function of the shape.
+ */
+int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                     void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                     int transpose, void* hip_stream);
+
+/*
+ * out = dequant(w) as bf16 [N, K] — the bit-exact unpack + affine dequant.
+ * Replaces mx.dequantize(w, scales, biases, group_size=64, bits=4) as used by the reference's
+ * exact-reference definition (tests/test_units.py:108) and qmm_packed.py:200-201 / 635-636.
+ *   Requires N >= 0, K % 64 == 0, group_size == 64, bits == 4, 16-byte aligned w and out.
+ */
+int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
+                         int64_t N, int64_t K, int group_size, int bits, void* hip_stream);
+
+/* Message for the last non-zero return on this host thread ("" if none). */
+const char* qmm4_last_error(void);
+
+/* Library ABI version (bumped when a signature above changes). */
+int qmm4_abi_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MI355X_QMM4_H */

@@ -1,0 +1,207 @@
+// C ABI of the packed 4-bit affine quantized matmul (declared in include/qmm4.h).
+//
+// Mirrors the reference's drop-in boundary: the quantized-linear call
+// mx.quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4)
+// (src/mlx_tree_spec/packed_linear.py:97) and its dispatch by row count
+// (packed_linear._call, packed_linear.py:83-104), with the argument checks the reference makes
+// with asserts and eligibility tests (qmm_packed.py:227, 705; packed_linear.py:49-58) turned into
+// error codes.
+#include <hip/hip_runtime.h>
+
+#include <algorithm>
+#include <cstdarg>
+#include <cstdio>
+#include <map>
+#include <mutex>
+#include <string>
+#include <utility>
+
+#include "qmm4.h"
+#include "qmm4_kernels.h"
+
+namespace {
+
+thread_local std::string g_last_error;
+
+int fail(int code, const char* fmt, ...) {
+  char buf[512];
+  va_list ap;
+  va_start(ap, fmt);
+  std::vsnprintf(buf, sizeof(buf), fmt, ap);
+  va_end(ap);
+  g_last_error = buf;
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  return fail(QMM4_ERR_HIP, "%s failed: %s (%d)", what, hipGetErrorString(e), (int)e);
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// Per-device facts, queried once.
+struct DeviceInfo {
+  int cus = 0;
+  int occ[3] = {0, 0, 0};  // resident skinny workgroups per CU, per variant
+};
+
+// Split-K workspace for one (device, stream): [counters | partials]. Counters are zeroed when the
+// buffer is (re)allocated and every launch leaves them at zero.
+struct Workspace {
+  void* base = nullptr;
+  size_t counter_bytes = 0;
+  size_t partial_bytes = 0;
+};
+
+std::mutex g_mu;
+std::map<int, DeviceInfo> g_dev;
+std::map<std::pair<int, hipStream_t>, Workspace> g_ws;
+
+int device_info(int dev, DeviceInfo** out) {
+  auto it = g_dev.find(dev);
+  if (it == g_dev.end()) {
+    DeviceInfo d;
+    hipError_t e = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev);
+    if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
+    for (int v = 0; v < 3; ++v) d.occ[v] = qmm4::skinny_occupancy(v);
+    it = g_dev.emplace(dev, d).first;
+  }
+  *out = &it->second;
+  return QMM4_OK;
+}
+
+int get_workspace(int dev, hipStream_t stream, size_t counter_bytes, size_t partial_bytes,
+                  uint32_t** cnt, float** part) {
+  Workspace& ws = g_ws[std::make_pair(dev, stream)];
+  if (ws.base == nullptr || ws.counter_bytes < counter_bytes || ws.partial_bytes < partial_bytes) {
+    const size_t cb = std::max(ws.counter_bytes, (counter_bytes + 255) / 256 * 256);
+    const size_t pb = std::max(ws.partial_bytes, (partial_bytes + 255) / 256 * 256);
+    if (ws.base != nullptr) {
+      hipError_t e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+      (void)hipFree(ws.base);
+      ws = Workspace();
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, cb + pb);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(QMM4_ERR_NOMEM, "workspace allocation of %zu bytes failed: %s", cb + pb,
+                  hipGetErrorString(e));
+    }
+    e = hipMemsetAsync(p, 0, cb, stream);
+    if (e != hipSuccess) {
+      (void)hipFree(p);
+      return hip_fail(e, "hipMemsetAsync(workspace counters)");
+    }
+    ws.base = p;
+    ws.counter_bytes = cb;
+    ws.partial_bytes = pb;
+  }
+  *cnt = static_cast<uint32_t*>(ws.base);
+  *part = reinterpret_cast<float*>(static_cast<char*>(ws.base) + ws.counter_bytes);
+  return QMM4_OK;
+}
+
+int check_format(int group_size, int bits, int transpose) {
+  if (bits != 4) return fail(QMM4_ERR_UNSUPPORTED, "bits=%d: only 4-bit codes are supported", bits);
+  if (group_size != 64)
+    return fail(QMM4_ERR_UNSUPPORTED, "group_size=%d: only group_size=64 is supported", group_size);
+  if (transpose != 1)
+    return fail(QMM4_ERR_UNSUPPORTED, "transpose=%d: only transpose=True (y = x @ w.T) is supported",
+                transpose);
+  return QMM4_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* qmm4_last_error(void) { return g_last_error.c_str(); }
+
+int qmm4_abi_version(void) { return 1; }
+
+int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                     void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                     int transpose, void* hip_stream) {
+  g_last_error.clear();
+  int rc = check_format(group_size, bits, transpose);
+  if (rc) return rc;
+  if (M < 0 || N < 0 || K <= 0)
+    return fail(QMM4_ERR_INVALID, "invalid shape M=%lld N=%lld K=%lld", (long long)M, (long long)N,
+                (long long)K);
+  if (K % 128 != 0)
+    return fail(QMM4_ERR_INVALID, "K=%lld must be a multiple of 128", (long long)K);
+  if (N % 16 != 0)
+    return fail(QMM4_ERR_INVALID, "N=%lld must be a multiple of 16", (long long)N);
+  if (M > (1LL << 30) || N > (1LL << 30) || K > (1LL << 30))
+    return fail(QMM4_ERR_INVALID, "shape M=%lld N=%lld K=%lld exceeds 2^30", (long long)M,
+                (long long)N, (long long)K);
+  if (M == 0 || N == 0) return QMM4_OK;
+  if (!x || !w || !scales || !biases || !y) return fail(QMM4_ERR_INVALID, "null pointer argument");
+  if (!aligned(x, 16) || !aligned(w, 16))
+    return fail(QMM4_ERR_INVALID, "x and w must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(y, 2))
+    return fail(QMM4_ERR_INVALID, "scales, biases and y must be 2-byte aligned");
+
+  hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* sb = static_cast<const uint16_t*>(scales);
+  const uint16_t* bb = static_cast<const uint16_t*>(biases);
+  uint16_t* yb = static_cast<uint16_t*>(y);
+
+  if (M > 64) {
+    hipError_t e = qmm4::launch_gemm(xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
+    if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
+    return QMM4_OK;
+  }
+
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceInfo* di = nullptr;
+  rc = device_info(dev, &di);
+  if (rc) return rc;
+
+  qmm4::SkinnyPlan plan;
+  plan.variant = qmm4::skinny_variant_for_rows((int)M, &plan.tile_cols);
+  plan.tiles = (int)((N + plan.tile_cols - 1) / plan.tile_cols);
+  plan.units = (long long)plan.tiles * (K / 128);
+  long long slots = (long long)di->cus * di->occ[plan.variant];
+  if (slots < 1) slots = 1;
+  plan.blocks = (int)(plan.units < slots ? plan.units : slots);
+
+  uint32_t* cnt = nullptr;
+  float* part = nullptr;
+  rc = get_workspace(dev, stream, (size_t)plan.tiles * sizeof(uint32_t),
+                     (size_t)plan.blocks * 2 * (size_t)M * plan.tile_cols * sizeof(float), &cnt, &part);
+  if (rc) return rc;
+  e = qmm4::launch_skinny(plan, xb, w, sb, bb, yb, part, cnt, (int)M, (int)N, (int)K, stream);
+  if (e != hipSuccess) return hip_fail(e, "skinny kernel launch");
+  return QMM4_OK;
+}
+
+int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
+                         int64_t N, int64_t K, int group_size, int bits, void* hip_stream) {
+  g_last_error.clear();
+  int rc = check_format(group_size, bits, 1);
+  if (rc) return rc;
+  if (N < 0 || K <= 0 || K % 64 != 0)
+    return fail(QMM4_ERR_INVALID, "invalid shape N=%lld K=%lld (K must be a positive multiple of 64)",
+                (long long)N, (long long)K);
+  if (N == 0) return QMM4_OK;
+  if (!w || !scales || !biases || !out) return fail(QMM4_ERR_INVALID, "null pointer argument");
+  if (!aligned(w, 16) || !aligned(out, 16))
+    return fail(QMM4_ERR_INVALID, "w and out must be 16-byte aligned");
+  if (!aligned(scales, 2) || !aligned(biases, 2))
+    return fail(QMM4_ERR_INVALID, "scales and biases must be 2-byte aligned");
+  hipError_t e = qmm4::launch_dequant(w, static_cast<const uint16_t*>(scales),
+                                      static_cast<const uint16_t*>(biases),
+                                      static_cast<uint16_t*>(out), N, K,
+                                      static_cast<hipStream_t>(hip_stream));
+  if (e != hipSuccess) return hip_fail(e, "dequant kernel launch");
+  return QMM4_OK;
+}
+
+}  // extern "C"

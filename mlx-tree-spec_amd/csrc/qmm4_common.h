@@ -1,0 +1,95 @@
+// Shared device helpers for the gfx950 packed 4-bit affine kernels.
+//
+// Format (MLX affine, 4 bits, group 64): w uint32 [N, K/8] holds q[n, 8c+i] in bits [4i, 4i+4) of
+// w[n, c] (src/mlx_tree_spec/qmm_packed.py:115, 200-201); scales/biases bf16 [N, K/64]; the
+// dequantized weight is bf16_rne(fp32(s) * q + fp32(b)) (qmm_packed.py:635-636).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace qmm4 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
+constexpr int kGroup = 64;  // quantization group along K
+
+__device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
+
+// Two fp32 values -> two bf16 (round to nearest even) in one dword, `a` in the low half.
+// Compiles to a single v_cvt_pk_bf16_f32.
+__device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
+  f32x2 v = {a, b};
+  bf16x2 r = __builtin_convertvector(v, bf16x2);
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+// Dequantize one packed word (codes for k = 8c .. 8c+7) with its group's scale and bias.
+// Result dword j holds bf16 for k = 8c+2j (low half) and 8c+2j+1 (high half).
+//
+// Even nibbles are isolated with one AND (bytes = q0, q2, q4, q6) and odd nibbles with another
+// AND left in place (bytes = 16*q1, ...); v_cvt_f32_ubyte{0..3} turns each byte into a float.
+// The odd codes are then scaled by s16 = s / 16, which is exact for every bf16 s (fp32 keeps
+// the bits through its subnormal range), so fma(16q, s/16, b) == fma(q, s, b): s*q is exact in
+// fp32 (8-bit by 4-bit significands) and the single rounding is the one of fp32(s*q + b).
+// 22 VALU instructions per word: 2 AND, 8 cvt, 8 FMA, 4 cvt_pk.
+__device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float s16, float b) {
+  uint32_t lo = w & 0x0F0F0F0Fu;
+  uint32_t hi = w & 0xF0F0F0F0u;
+  // Keep the two masks opaque so the backend emits v_cvt_f32_ubyteN on them instead of
+  // re-deriving each nibble with v_bfe_u32 + v_cvt_f32_ubyte0 (one extra op per code).
+  asm volatile("" : "+v"(lo), "+v"(hi));
+  const float q0 = (float)(lo & 0xFFu), q2 = (float)((lo >> 8) & 0xFFu);
+  const float q4 = (float)((lo >> 16) & 0xFFu), q6 = (float)(lo >> 24);
+  const float h1 = (float)(hi & 0xFFu), h3 = (float)((hi >> 8) & 0xFFu);
+  const float h5 = (float)((hi >> 16) & 0xFFu), h7 = (float)(hi >> 24);
+  u32x4 r;
+  r.x = pack_bf16x2(__builtin_fmaf(q0, s, b), __builtin_fmaf(h1, s16, b));
+  r.y = pack_bf16x2(__builtin_fmaf(q2, s, b), __builtin_fmaf(h3, s16, b));
+  r.z = pack_bf16x2(__builtin_fmaf(q4, s, b), __builtin_fmaf(h5, s16, b));
+  r.w = pack_bf16x2(__builtin_fmaf(q6, s, b), __builtin_fmaf(h7, s16, b));
+  return r;
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
+
+// MFMA tiles used here (gfx950 bf16, fp32 accumulation).
+//   16x16x32: A lane l holds row l%16, k-chunk l/16 (8 values); B lane l holds column l%16,
+//             k-chunk l/16; D lane l, element r holds row 4*(l/16)+r, column l%16.
+//   32x32x16: A lane l holds row l%32, k-chunk l/32; B lane l holds column l%32, k-chunk l/32;
+//             D lane l, element r holds row 8*(r/4) + 4*(l/32) + r%4, column l%32.
+// Products pair A and B values held at the same (lane group, element) position, so any
+// permutation of K applied identically to both operands gives the same sum; the kernels use
+// that freedom to give each lane contiguous packed words.
+template <int MT>
+struct Mfma;
+
+template <>
+struct Mfma<16> {
+  typedef f32x4 Acc;
+  static constexpr int kAcc = 4;
+  __device__ static __forceinline__ Acc mma(bf16x8 a, bf16x8 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int row(int lane, int r) { return 4 * (lane >> 4) + r; }
+};
+
+template <>
+struct Mfma<32> {
+  typedef f32x16 Acc;
+  static constexpr int kAcc = 16;
+  __device__ static __forceinline__ Acc mma(bf16x8 a, bf16x8 b, Acc c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+  __device__ static __forceinline__ int row(int lane, int r) {
+    return 8 * (r >> 2) + 4 * (lane >> 5) + (r & 3);
+  }
+};
+
+}  // namespace qmm4

@@ -1,0 +1,16 @@
+"""MI355X (gfx950) packed 4-bit affine quantized matmul in MLX's format.
+
+    from mlx_tree_spec_amd import quantized_matmul, dequantize, QuantizedLinear, install
+
+All compute runs in libqmm4.so (hand-written HIP kernels, C ABI in include/qmm4.h); importing
+this package does not load it, the first call does, and fails loudly if it is not built.
+"""
+
+from .packed_linear import STATS, QuantizedLinear, eligible, install
+from .qmm import dequantize, pack_nax, quantized_matmul, unpack_nax
+
+__all__ = [
+    "quantized_matmul", "dequantize", "pack_nax", "unpack_nax",
+    "QuantizedLinear", "eligible", "install", "STATS",
+]
+__version__ = "0.1.0"

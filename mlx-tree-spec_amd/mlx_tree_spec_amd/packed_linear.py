@@ -1,0 +1,154 @@
+"""Quantized-linear drop-in: a torch module whose call is the gfx950 packed 4-bit kernel.
+
+Mirrors src/mlx_tree_spec/packed_linear.py:
+  eligible(mod)        -> packed_linear.eligible (49-58): 4-bit affine with biases, no linear
+                          bias, N % 32 == 0, K % 128 == 0
+  install(model)       -> packed_linear.install (136-179): prepares every eligible module and
+                          prebinds its launcher; returns the same summary dict
+  QuantizedLinear      -> mlx.nn.QuantizedLinear (weight uint32 [N, K/8], scales and biases
+                          bf16 [N, K/64]) with __call__ = _call
+  _call(mod, x)        -> packed_linear._call (83-104): rows = prod(x.shape[:-1]), dispatch by rows
+  STATS                -> per-path call counters (packed_linear.py:46)
+
+Differences by design (MI355X-first):
+  * no relayout: the kernels read MLX's [N, K/8] layout directly, so install() keeps the weights
+    as they are (no transient copy) instead of rewriting them with pack_nax;
+  * no install-time timing race between kernels: the kernel is a fixed function of the row count
+    (M <= SKINNY_MAX_ROWS: the HBM-bound skinny kernel; larger M: the MFMA GEMM), decided inside
+    the library;
+  * the prebound launcher skips the per-call argument checks (weights were validated once).
+"""
+
+from __future__ import annotations
+
+import math
+from collections import defaultdict
+
+import torch
+
+from . import _lib
+from .qmm import quantized_matmul
+
+SKINNY_MAX_ROWS = 64  # rows <= this take the skinny kernel (the reference's PREFILL_M is 64)
+STATS: dict[str, int] = defaultdict(int)
+
+
+class QuantizedLinear(torch.nn.Module):
+    """y = x @ dequant(weight).T (+ bias) for MLX-format affine 4-bit weights."""
+
+    def __init__(self, input_dims: int, output_dims: int, bias: bool = False, group_size: int = 64,
+                 bits: int = 4, mode: str = "affine", device=None):
+        super().__init__()
+        if input_dims % 32:
+            raise ValueError(f"input_dims={input_dims} must be a multiple of 32 for {bits}-bit packing")
+        self.group_size, self.bits, self.mode = group_size, bits, mode
+        self.register_buffer("weight", torch.zeros(output_dims, input_dims * bits // 32, dtype=torch.int32, device=device))
+        self.register_buffer("scales", torch.zeros(output_dims, input_dims // group_size, dtype=torch.bfloat16, device=device))
+        self.register_buffer("biases", torch.zeros(output_dims, input_dims // group_size, dtype=torch.bfloat16, device=device))
+        self.bias = torch.nn.Parameter(torch.zeros(output_dims, dtype=torch.bfloat16, device=device)) if bias else None
+
+    @classmethod
+    def from_quantized(cls, weight: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                       group_size: int = 64, bits: int = 4, bias: torch.Tensor | None = None) -> "QuantizedLinear":
+        n, kw = weight.shape
+        mod = cls(kw * 32 // bits, n, bias=bias is not None, group_size=group_size, bits=bits,
+                  device=weight.device)
+        mod.weight = weight.view(torch.int32) if weight.dtype == torch.uint32 else weight
+        mod.scales, mod.biases = scales, biases
+        if bias is not None:
+            mod.bias = torch.nn.Parameter(bias)
+        return mod
+
+    @property
+    def input_dims(self) -> int:
+        return self.weight.shape[1] * 32 // self.bits
+
+    @property
+    def output_dims(self) -> int:
+        return self.weight.shape[0]
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        return _call(self, x)
+
+
+def eligible(mod) -> bool:
+    """packed_linear.eligible: the modules the packed kernels take."""
+    return (
+        isinstance(mod, QuantizedLinear)
+        and mod.bits == 4
+        and getattr(mod, "mode", "affine") == "affine"
+        and mod.biases is not None
+        and mod.bias is None
+        and mod.weight.shape[0] % 32 == 0
+        and (mod.weight.shape[1] * 8) % 128 == 0
+    )
+
+
+def _launcher(mod: QuantizedLinear):
+    """mod's matmul with weights, shape and library bound: per call only x is checked."""
+    w, s, b = mod.weight, mod.scales, mod.biases
+    n, k, gs = mod.output_dims, mod.input_dims, mod.group_size
+    wp, sp, bp = w.data_ptr(), s.data_ptr(), b.data_ptr()
+    dev = w.device
+    fn = _lib.load().qmm4_affine_bf16
+
+    def run(x: torch.Tensor) -> torch.Tensor:
+        if x.dtype != torch.bfloat16 or x.shape[-1] != k or x.device != dev:
+            raise ValueError(f"[QuantizedLinear] expected bfloat16 (..., {k}) on {dev}, got "
+                             f"{x.dtype} {tuple(x.shape)} on {x.device}")
+        x2 = x.reshape(-1, k)
+        if not x2.is_contiguous() or x2.data_ptr() % 16:
+            x2 = x2.contiguous()
+        y = torch.empty((*x.shape[:-1], n), dtype=torch.bfloat16, device=dev)
+        rc = fn(x2.data_ptr(), wp, sp, bp, y.data_ptr(), x2.shape[0], n, k, gs, 4, 1,
+                torch.cuda.current_stream(dev).cuda_stream)
+        _lib.check(rc, "QuantizedLinear")
+        return y
+
+    return run
+
+
+def _call(self: QuantizedLinear, x: torch.Tensor) -> torch.Tensor:
+    sh = x.shape
+    rows = math.prod(sh[:-1])
+    STATS["skinny" if rows <= SKINNY_MAX_ROWS else "gemm"] += 1
+    run = self.__dict__.get("_fast")
+    if run is not None:
+        y = run(x)
+    else:
+        y = quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
+                             group_size=self.group_size, bits=self.bits, mode=self.mode)
+    if self.bias is not None:
+        y = y + self.bias
+    return y
+
+
+def install(model: torch.nn.Module, verbose: bool = True) -> dict:
+    """Prepare every eligible QuantizedLinear of `model` for the packed kernels.
+
+    Weights must already be on the HIP device. Each module's buffers are made contiguous and
+    16-byte aligned once and a launcher with them bound is attached, so a forward's calls skip
+    the generic argument checks. Returns the reference's summary dict.
+    """
+    before = torch.cuda.memory_allocated() if torch.cuda.is_available() else 0
+    groups: dict[tuple[int, int], int] = defaultdict(int)
+    packed = 0
+    for _, mod in model.named_modules():
+        if not eligible(mod) or "_fast" in mod.__dict__:
+            continue
+        if mod.weight.device.type != "cuda":
+            raise ValueError("install(): move the model to the HIP device first")
+        if mod.scales.dtype != torch.bfloat16 or mod.biases.dtype != torch.bfloat16:
+            raise ValueError("install(): scales and biases must be bfloat16")
+        for name in ("weight", "scales", "biases"):
+            t = getattr(mod, name)
+            if not t.is_contiguous() or t.data_ptr() % 16:
+                setattr(mod, name, t.contiguous())
+        object.__setattr__(mod, "_fast", _launcher(mod))
+        groups[(mod.input_dims, mod.output_dims)] += 1
+        packed += 1
+    if verbose:
+        for (k, n), c in sorted(groups.items()):
+            print(f"  packed {k:>6}->{n:<6} x{c}")
+    after = torch.cuda.memory_allocated() if torch.cuda.is_available() else 0
+    return dict(packed=packed, memory_before_gb=before / 1e9, memory_after_gb=after / 1e9)

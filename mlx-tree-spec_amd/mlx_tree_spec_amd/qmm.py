@@ -1,0 +1,138 @@
+"""The quantized-linear operator on PyTorch-ROCm tensors, backed by libqmm4.so (gfx950 HIP).
+
+Mirrors the reference's calls:
+  quantized_matmul(x, w, scales, biases, transpose=True, group_size=64, bits=4)
+      == mx.quantized_matmul as called at src/mlx_tree_spec/packed_linear.py:97
+  dequantize(w, scales, biases, group_size=64, bits=4)
+      == mx.dequantize as used by the exact reference at tests/test_units.py:108
+  pack_nax / unpack_nax
+      == the reference's install-time relayout and its inverse (qmm_packed.py:223-232,
+         packed_linear.py:72-80), kept for interoperability: the gfx950 kernels read MLX's own
+         [N, K/8] layout, so weights in the reference's packed layout are converted back once.
+
+Tensors: x bfloat16 (..., K) on a HIP device; w int32 or uint32 [N, K/8] (the bits are used as
+is); scales and biases bfloat16 [N, K/64]. Output bfloat16 (..., N), allocated here, written
+asynchronously on the current stream of x's device.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+_W_DTYPES = (torch.int32, torch.uint32)
+
+
+def _check_format(group_size: int, bits: int, transpose: bool = True, mode: str = "affine") -> None:
+    if mode != "affine":
+        raise NotImplementedError(f"mode={mode!r}: only 'affine' quantization is supported")
+    if bits != 4:
+        raise NotImplementedError(f"bits={bits}: only 4-bit codes are supported")
+    if group_size != 64:
+        raise NotImplementedError(f"group_size={group_size}: only group_size=64 is supported")
+    if not transpose:
+        raise NotImplementedError("transpose=False: only y = x @ dequant(w).T is supported")
+
+
+def _check_weights(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, k: int | None,
+                   group_size: int, bits: int, what: str) -> tuple[int, int]:
+    if w.dim() != 2 or w.dtype not in _W_DTYPES:
+        raise ValueError(f"[{what}] w must be a 2-D int32/uint32 tensor, got {tuple(w.shape)} {w.dtype}")
+    n, kw = w.shape
+    kk = kw * 32 // bits
+    if k is not None and kk != k:
+        raise ValueError(f"[{what}] x.shape[-1]={k} does not match w.shape[-1]*32/bits={kk}")
+    if scales is None or biases is None:
+        raise ValueError(f"[{what}] affine quantization needs both scales and biases")
+    for name, t in (("scales", scales), ("biases", biases)):
+        if t.dtype != torch.bfloat16:
+            raise ValueError(f"[{what}] {name} must be bfloat16, got {t.dtype}")
+        if tuple(t.shape) != (n, kk // group_size):
+            raise ValueError(f"[{what}] {name} shape {tuple(t.shape)} != {(n, kk // group_size)}")
+    return n, kk
+
+
+def _check_device(what: str, *ts: torch.Tensor) -> torch.device:
+    dev = ts[0].device
+    if dev.type != "cuda":
+        raise ValueError(f"[{what}] tensors must be on a HIP device (got {dev}); there is no CPU path")
+    for t in ts[1:]:
+        if t.device != dev:
+            raise ValueError(f"[{what}] all tensors must be on {dev}, got {t.device}")
+    return dev
+
+
+def _contig(t: torch.Tensor) -> torch.Tensor:
+    return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
+
+
+def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                     transpose: bool = True, group_size: int = 64, bits: int = 4,
+                     mode: str = "affine") -> torch.Tensor:
+    """y = x @ dequant(w).T in bf16 with fp32 accumulation (HIP kernels; no fallback)."""
+    _check_format(group_size, bits, transpose, mode)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"[quantized_matmul] x must be bfloat16, got {x.dtype}")
+    if x.dim() < 1:
+        raise ValueError("[quantized_matmul] x must have at least one dimension")
+    k = x.shape[-1]
+    n, _ = _check_weights(w, scales, biases, k, group_size, bits, "quantized_matmul")
+    dev = _check_device("quantized_matmul", x, w, scales, biases)
+    x2 = _contig(x.reshape(-1, k))
+    m = x2.shape[0]
+    w = _contig(w)
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    y = torch.empty((*x.shape[:-1], n), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.qmm4_affine_bf16(x2.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                                  y.data_ptr(), m, n, k, group_size, bits, 1, stream)
+    _lib.check(rc, "quantized_matmul")
+    return y
+
+
+def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = 64,
+               bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """bf16 [N, K] with w_deq = bf16_rne(fp32(s) * q + fp32(b)), bit-exact (HIP kernel)."""
+    _check_format(group_size, bits, True, mode)
+    n, k = _check_weights(w, scales, biases, None, group_size, bits, "dequantize")
+    dev = _check_device("dequantize", w, scales, biases)
+    w = _contig(w)
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    out = torch.empty((n, k), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.dequant4_affine_bf16(w.data_ptr(), scales.data_ptr(), biases.data_ptr(), out.data_ptr(),
+                                      n, k, group_size, bits, stream)
+    _lib.check(rc, "dequantize")
+    return out
+
+
+def pack_nax(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor):
+    """MLX layout -> the reference's packed layout (qmm_packed.py:223-232), flat tensors:
+    wq2[t][kb][r][j] = w[32t + r][2kb + j], sp2[t][g][r] = s[32t + r][g] (same for biases)."""
+    n, kw = w.shape
+    if n % 32 or kw % 2:
+        raise ValueError(f"[pack_nax] need N % 32 == 0 and K % 16 == 0, got w {tuple(w.shape)}")
+    g = scales.shape[1]
+    wi = w.view(torch.int32) if w.dtype == torch.uint32 else w  # uint32 has few torch kernels
+    wq2 = wi.reshape(n // 32, 32, kw // 2, 2).permute(0, 2, 1, 3).contiguous().reshape(-1).view(w.dtype)
+    sp2 = scales.reshape(n // 32, 32, g).permute(0, 2, 1).contiguous().reshape(-1)
+    bp2 = biases.reshape(n // 32, 32, g).permute(0, 2, 1).contiguous().reshape(-1)
+    return wq2, sp2, bp2
+
+
+def unpack_nax(wq2: torch.Tensor, sp2: torch.Tensor, bp2: torch.Tensor, n: int):
+    """The reference's packed layout -> MLX layout (packed_linear._unpacked, packed_linear.py:72-80)."""
+    kw = wq2.numel() // n
+    g = sp2.numel() // n
+    wi = wq2.view(torch.int32) if wq2.dtype == torch.uint32 else wq2
+    w = wi.reshape(n // 32, kw // 2, 32, 2).permute(0, 2, 1, 3).contiguous().reshape(n, kw).view(wq2.dtype)
+    s = sp2.reshape(n // 32, g, 32).permute(0, 2, 1).contiguous().reshape(n, g)
+    b = bp2.reshape(n // 32, g, 32).permute(0, 2, 1).contiguous().reshape(n, g)
+    return w, s, b

@@ -1,0 +1,98 @@
+"""The C ABI library: loads, exports every declared symbol, rejects bad arguments (CPU only —
+every call here fails validation or is a no-op before any GPU work)."""
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from mlx_tree_spec_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "qmm4.h")
+
+
+def declared_functions():
+    src = open(HEADER).read()
+    src = re.sub(r"/\*.*?\*/", "", src, flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:const\s+)?\w+\**\s+\**(\w+)\s*\(", src, flags=re.M)))
+
+
+def test_header_declares_expected_api():
+    assert declared_functions() == sorted(["qmm4_affine_bf16", "dequant4_affine_bf16", "qmm4_last_error",
+                                           "qmm4_abi_version"])
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_functions():
+        assert hasattr(lib, name), name
+        assert name in _lib.SIGNATURES
+    assert lib.qmm4_abi_version() == 1
+
+
+def call(M=4, N=32, K=128, gs=64, bits=4, transpose=1, ptr=0x10000, y=0x20000):
+    lib = _lib.load()
+    return lib.qmm4_affine_bf16(ptr, ptr, ptr, ptr, y, M, N, K, gs, bits, transpose, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(bits=3), _lib.QMM4_ERR_UNSUPPORTED, "bits=3"),
+    (dict(bits=8), _lib.QMM4_ERR_UNSUPPORTED, "bits=8"),
+    (dict(gs=32), _lib.QMM4_ERR_UNSUPPORTED, "group_size=32"),
+    (dict(gs=128), _lib.QMM4_ERR_UNSUPPORTED, "group_size=128"),
+    (dict(transpose=0), _lib.QMM4_ERR_UNSUPPORTED, "transpose=0"),
+    (dict(K=192), _lib.QMM4_ERR_INVALID, "K=192"),
+    (dict(K=0), _lib.QMM4_ERR_INVALID, "invalid shape"),
+    (dict(N=24), _lib.QMM4_ERR_INVALID, "N=24"),
+    (dict(M=-1), _lib.QMM4_ERR_INVALID, "invalid shape"),
+    (dict(M=1 << 31), _lib.QMM4_ERR_INVALID, "exceeds"),
+    (dict(ptr=0), _lib.QMM4_ERR_INVALID, "null pointer"),
+    (dict(ptr=0x10008), _lib.QMM4_ERR_INVALID, "16-byte aligned"),
+    (dict(y=0x20001), _lib.QMM4_ERR_INVALID, "2-byte aligned"),
+])
+def test_qmm_rejects(kw, code, msg):
+    assert call(**kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_qmm_empty_is_noop():
+    assert call(M=0, ptr=0) == _lib.QMM4_OK
+    assert call(N=0, ptr=0) == _lib.QMM4_OK
+    assert _lib.last_error() == ""
+
+
+def test_dequant_rejects():
+    lib = _lib.load()
+    p = 0x10000
+    assert lib.dequant4_affine_bf16(p, p, p, p, 8, 96, 64, 4, None) == _lib.QMM4_ERR_INVALID
+    assert "K" in _lib.last_error()
+    assert lib.dequant4_affine_bf16(p, p, p, p, 8, 128, 64, 2, None) == _lib.QMM4_ERR_UNSUPPORTED
+    assert lib.dequant4_affine_bf16(0, p, p, p, 8, 128, 64, 4, None) == _lib.QMM4_ERR_INVALID
+    assert lib.dequant4_affine_bf16(p + 4, p, p, p, 8, 128, 64, 4, None) == _lib.QMM4_ERR_INVALID
+    assert lib.dequant4_affine_bf16(0, 0, 0, 0, 0, 128, 64, 4, None) == _lib.QMM4_OK
+
+
+def test_error_message_is_thread_local():
+    import threading
+
+    assert call(bits=3) == _lib.QMM4_ERR_UNSUPPORTED
+    seen = []
+    t = threading.Thread(target=lambda: seen.append(_lib.last_error()))
+    t.start()
+    t.join()
+    assert seen == [""] and "bits=3" in _lib.last_error()
+
+
+def test_check_maps_codes():
+    call(bits=3)
+    with pytest.raises(NotImplementedError):
+        _lib.check(_lib.QMM4_ERR_UNSUPPORTED, "t")
+    with pytest.raises(ValueError):
+        _lib.check(_lib.QMM4_ERR_INVALID, "t")
+    with pytest.raises(MemoryError):
+        _lib.check(_lib.QMM4_ERR_NOMEM, "t")
+    with pytest.raises(RuntimeError):
+        _lib.check(_lib.QMM4_ERR_HIP, "t")
+    _lib.check(_lib.QMM4_OK, "t")

@@ -1,0 +1,221 @@
+"""Parity of the gfx950 kernels with the oracle, through the C ABI (needs an MI355X).
+
+Bars:
+  * dequantize: bit-exact against the exact-rational brute-force table, and against the oracle
+    over every finite bf16 scale and random model-sized weights;
+  * quantized_matmul: the north-star tolerance against the fp32-accumulated reference
+    (max|y-ref|/max|ref| <= 1e-2, mean|y-ref|/mean|ref| <= 2e-3), and, much tighter, per element:
+    at least 99% of outputs equal bf16_rne(ref) and every other output is one bf16 ulp from it
+    (only the fp32 accumulation order differs from the oracle);
+  * size-independent properties at the full workload sizes: determinism, y(2x) == 2 y(x).
+"""
+
+import os
+import sys
+
+import numpy as np
+import pytest
+import torch
+
+import golden_io
+from mlx_tree_spec_amd import STATS, QuantizedLinear, dequantize, install, quantized_matmul
+from oracle import cpu
+from oracle import qmm4_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+
+
+def note(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def bf16_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def u32_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(DEV)
+
+
+def host_bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def gpu_qmm(x, w, s, b):
+    y = quantized_matmul(bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b))
+    return host_bits(y)
+
+
+def check_qmm(y_bits, ref, what=""):
+    ref = np.asarray(ref, dtype=np.float64)
+    y = O.bf16_bits_to_f32(y_bits).astype(np.float64)
+    mx, mn = O.max_rel(y, ref), O.mean_rel(y, ref)
+    rne = O.f32_to_bf16_bits(ref.astype(np.float32))
+    mism = y_bits != rne
+    # Any other output must be a bf16 neighbour of bf16_rne(ref) (same sign, one ulp away).
+    step = np.abs(y_bits.astype(np.int32) - rne.astype(np.int32))
+    far = mism & ((step != 1) | ((y_bits >> 15) != (rne >> 15)))
+    note(f"  {what} max_rel={mx:.2e} mean_rel={mn:.2e} mismatches={int(mism.sum())}/{mism.size} far={int(far.sum())}")
+    assert mx <= O.MAX_REL_TOL and mn <= O.MEAN_REL_TOL
+    assert int(mism.sum()) <= max(2, mism.size // 100)
+    assert not far.any()
+
+
+def test_native_library_is_loaded():
+    x, w, s, b = O.make_inputs(1, 128, 16, seed=0)
+    gpu_qmm(x, w, s, b)
+    maps = open("/proc/self/maps").read()
+    assert "libqmm4.so" in maps
+
+
+# ----------------------------------------------------------------------------- dequant
+def test_dequant_bruteforce_table():
+    w, s, b, expected, _ = golden_io.dequant_table_weights()
+    got = host_bits(dequantize(u32_dev(w), bf16_dev(s), bf16_dev(b)))
+    assert np.array_equal(got, expected)
+
+
+@pytest.mark.parametrize("bias_kind", ["model", "random"])
+def test_dequant_every_finite_bf16_scale(bias_kind):
+    allbits = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    s = allbits[((allbits >> 7) & 0xFF) != 0xFF]
+    n = s.size
+    rng = np.random.default_rng(11)
+    if bias_kind == "model":
+        b = O.f32_to_bf16_bits(-8 * O.bf16_bits_to_f32(s) + rng.standard_normal(n).astype(np.float32) * 1e-3)
+        b = np.where(((b >> 7) & 0xFF) == 0xFF, np.uint16(0), b)
+    else:
+        b = rng.integers(0, 65536, n).astype(np.uint16)
+        b = np.where(((b >> 7) & 0xFF) == 0xFF, np.uint16(0x3F80), b)
+    codes = np.tile(np.arange(16, dtype=np.uint8), (n, 4))
+    w = O.pack_codes(codes)
+    s2, b2 = s.reshape(n, 1), b.reshape(n, 1)
+    got = host_bits(dequantize(u32_dev(w), bf16_dev(s2), bf16_dev(b2)))
+    assert np.array_equal(got, O.dequantize(w, s2, b2))
+
+
+@pytest.mark.parametrize("n,k", [(16, 64), (48, 192), (512, 5120), (1000, 17408)])
+def test_dequant_random(n, k):
+    _, w, s, b = O.make_inputs(1, k, n, seed=n)
+    got = host_bits(dequantize(u32_dev(w), bf16_dev(s), bf16_dev(b)))
+    assert np.array_equal(got, O.dequantize(w, s, b))
+
+
+# ----------------------------------------------------------------------------- small / golden
+@pytest.mark.parametrize("case", [c for c in golden_io.qmm_cases() if c["k"] % 128 == 0 and c["n"] % 16 == 0],
+                         ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
+def test_qmm_bruteforce_cases(case):
+    y = gpu_qmm(case["x"], case["w"], case["s"], case["b"])
+    check_qmm(y, case["exact"], "golden")
+
+
+ROWS = [1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 24, 31, 32, 33, 40, 47, 48, 63, 64]
+
+
+@pytest.mark.parametrize("m", ROWS)
+def test_qmm_skinny_rows(m):
+    x, w, s, b = O.make_inputs(m, 512, 272, seed=m)  # N % 32 == 16: a half column tile
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"M={m}")
+
+
+@pytest.mark.parametrize("m", [1, 4, 16, 32, 64])
+@pytest.mark.parametrize("k,n", [(128, 16), (5120, 1024), (17408, 256), (1024, 4112)])
+def test_qmm_skinny_shapes(m, k, n):
+    x, w, s, b = O.make_inputs(m, k, n, seed=k + n + m)
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m", [64, 100, 2048])
+@pytest.mark.parametrize("k,n", [(512, 128), (1024, 192)])
+def test_reference_prefill_kernel_shapes(m, k, n):
+    """The shapes of the reference's only kernel test (tests/test_units.py:90-110): x is
+    (1, m, k) with sigma 0.5."""
+    x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=0)
+    y = quantized_matmul(bf16_dev(x).reshape(1, m, k), u32_dev(w), bf16_dev(s), bf16_dev(b))
+    assert tuple(y.shape) == (1, m, n)
+    check_qmm(host_bits(y).reshape(m, n), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}")
+
+
+@pytest.mark.parametrize("m,k,n", [(65, 5120, 1024), (255, 128, 528), (256, 256, 256), (257, 1024, 784),
+                                   (1024, 5120, 1040), (4096, 1024, 512)])
+def test_qmm_gemm_shapes(m, k, n):
+    x, w, s, b = O.make_inputs(m, k, n, seed=m + k)
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}")
+
+
+# ----------------------------------------------------------------------------- workloads
+def workload_ref(x, w, s, b):
+    return cpu.qmm_f32(x, w, s, b).astype(np.float64)
+
+
+@pytest.mark.parametrize("index,m", [(0, 16), (1, 1), (1, 2), (1, 4), (2, 64), (3, 32)])
+def test_workload_full(index, m):
+    note(f"workload {index} M={m}")
+    x, w, s, b = O.config_inputs(index, m=m)
+    y = gpu_qmm(x, w, s, b)
+    check_qmm(y, workload_ref(x, w, s, b), f"c{index} M={m}")
+
+
+def test_workload_prefill_sampled_rows():
+    """The 4096 x 5120 -> 17408 prefill GEMM on the GPU; 256 sampled rows against the oracle."""
+    x, w, s, b = O.config_inputs(4)
+    y = gpu_qmm(x, w, s, b)
+    rows = np.random.default_rng(4).choice(x.shape[0], 256, replace=False)
+    rows.sort()
+    check_qmm(y[rows], workload_ref(x[rows], w, s, b), "c4 sampled rows")
+
+
+@pytest.mark.parametrize("index,m", [(0, 16), (1, 4), (2, 64), (3, 32), (4, 4096)])
+def test_workload_deterministic_and_pow2_linear(index, m):
+    x, w, s, b = O.config_inputs(index, m=m)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y1 = host_bits(quantized_matmul(xd, wd, sd, bd))
+    y2 = host_bits(quantized_matmul(xd, wd, sd, bd))
+    assert np.array_equal(y1, y2)
+    y2x = host_bits(quantized_matmul(xd * 2, wd, sd, bd))
+    assert np.array_equal(O.bf16_bits_to_f32(y2x), 2 * O.bf16_bits_to_f32(y1))
+
+
+# ----------------------------------------------------------------------------- host integration
+def test_side_stream_and_workspace_growth():
+    cases = [O.make_inputs(16, 5120, 512, seed=1), O.make_inputs(64, 17408, 1024, seed=2), O.make_inputs(3, 256, 64, seed=3)]
+    side = torch.cuda.Stream()
+    for x, w, s, b in cases + cases[::-1]:
+        ref = O.quantized_matmul_exact(x, w, s, b)
+        check_qmm(gpu_qmm(x, w, s, b), ref, "default stream")
+        with torch.cuda.stream(side):
+            y = quantized_matmul(bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b))
+        side.synchronize()
+        check_qmm(host_bits(y), ref, "side stream")
+
+
+def test_noncontiguous_and_empty():
+    x, w, s, b = O.make_inputs(8, 256, 64, seed=9)
+    xbig = bf16_dev(np.concatenate([x, x], axis=1))
+    xv = xbig[:, 256:]  # non-contiguous view
+    y = quantized_matmul(xv, u32_dev(w), bf16_dev(s), bf16_dev(b))
+    check_qmm(host_bits(y), O.quantized_matmul_exact(x, w, s, b), "strided x")
+    y0 = quantized_matmul(bf16_dev(x[:0]), u32_dev(w), bf16_dev(s), bf16_dev(b))
+    assert tuple(y0.shape) == (0, 64)
+
+
+def test_quantized_linear_install():
+    k, n = 1024, 256
+    mods = []
+    for seed in range(3):
+        _, w, s, b = O.make_inputs(1, k, n, seed=seed)
+        mods.append(QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(s), bf16_dev(b)))
+    model = torch.nn.Sequential(*mods)
+    summary = install(model, verbose=False)
+    assert summary["packed"] == 3
+    for m in (1, 16, 100):
+        x, *_ = O.make_inputs(m, k, n, seed=m)
+        xd = bf16_dev(x).reshape(1, m, k)
+        before = dict(STATS)
+        y = mods[0](xd)
+        key = "skinny" if m <= 64 else "gemm"
+        assert STATS[key] == before.get(key, 0) + 1
+        ref = quantized_matmul(xd, mods[0].weight, mods[0].scales, mods[0].biases)
+        assert torch.equal(y.view(torch.int16), ref.view(torch.int16))

@@ -1,0 +1,210 @@
+"""The oracle, pinned before it is trusted (CPU only).
+
+How each oracle function is pinned:
+  unpack_codes / pack_codes  bytes-view decode of qmm_packed.py:115-116 (independent of shifts);
+                             brute-force fixture; round trip
+  f32_to_bf16_bits           torch's own fp32 -> bf16 conversion (round to nearest even)
+  dequantize                 exact-rational brute-force fixture (incl. 257 double-rounding
+                             entries); closed forms s=1,b=0 -> q; q=0 -> b; s=0 -> b;
+                             group mapping with distinct per-group scales
+  quantized_matmul(_exact)   brute-force fixture (exact rational sums); one-hot x picks single
+                             dequantized weights; integer codes with s=1, b=0 against integer
+                             arithmetic; linearity and power-of-two scaling
+  pack_nax / unpack_nax      index-loop fixture of qmm_packed.py:224-231; round trip
+  metrics, byte/flop counts  closed forms (the workload table's published byte counts)
+  C restatement (cpu.py)     against the numpy oracle (bit-exact dequant, tolerance on y)
+A planted mistake in the oracle (reversed nibble order, raw-code accumulation) must fail.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+import golden_io
+from oracle import cpu
+from oracle import qmm4_oracle as O
+
+
+def bytes_view_codes(w):
+    """Codes from the little-endian bytes: byte j of word c -> k = 8c+2j (low), 8c+2j+1 (high)."""
+    b = np.ascontiguousarray(w, dtype="<u4").view(np.uint8).reshape(w.shape[0], -1)
+    out = np.empty((w.shape[0], b.shape[1] * 2), dtype=np.uint8)
+    out[:, 0::2] = b & 0xF
+    out[:, 1::2] = b >> 4
+    return out
+
+
+def test_unpack_codes_matches_bytes_view():
+    rng = np.random.default_rng(1)
+    w = rng.integers(0, 2**32, size=(37, 24), dtype=np.uint32)
+    assert np.array_equal(O.unpack_codes(w), bytes_view_codes(w))
+    assert np.array_equal(O.pack_codes(O.unpack_codes(w)), w)
+
+
+def test_unpack_codes_single_word():
+    w = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.uint32)
+    assert O.unpack_codes(w).tolist() == [list(range(16))]
+
+
+def test_bf16_rounding_matches_torch():
+    rng = np.random.default_rng(2)
+    bits = rng.integers(0, 2**32, size=200000, dtype=np.uint32)
+    f = bits.view(np.float32)
+    f = f[np.isfinite(f)]
+    ties = (rng.integers(0, 2**16, size=5000, dtype=np.uint32) << 16 | 0x8000).view(np.float32)
+    ties = ties[np.isfinite(ties)]
+    for arr in (f, ties, np.array([0.0, -0.0, 1e-40, -1e-40, 3.4e38, -3.4e38], np.float32)):
+        ref = torch.from_numpy(arr.copy()).to(torch.bfloat16).view(torch.int16).numpy().view(np.uint16)
+        assert np.array_equal(O.f32_to_bf16_bits(arr), ref)
+    nan = O.f32_to_bf16_bits(np.array([np.nan], np.float32))
+    assert np.isnan(O.bf16_bits_to_f32(nan)).all()
+
+
+def test_dequant_matches_bruteforce_table():
+    w, s, b, expected, single = golden_io.dequant_table_weights()
+    got = O.dequantize(w, s, b)
+    assert np.array_equal(got, expected)
+    # The table holds entries where rounding s*q+b straight to bf16 would differ: the oracle must
+    # follow the reference's fp32-then-bf16 rounding there.
+    assert (expected != single).sum() > 100
+    assert not np.array_equal(got, single)
+
+
+def test_dequant_closed_forms():
+    rng = np.random.default_rng(3)
+    n, k = 8, 256
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    q = O.unpack_codes(w).astype(np.float32)
+    one = np.full((n, k // 64), 0x3F80, np.uint16)
+    zero = np.zeros((n, k // 64), np.uint16)
+    assert np.array_equal(O.bf16_bits_to_f32(O.dequantize(w, one, zero)), q)
+    b = O.f32_to_bf16_bits(rng.standard_normal((n, k // 64)).astype(np.float32))
+    assert np.array_equal(O.dequantize(w, zero, b), np.repeat(b, 64, axis=1))
+    assert np.array_equal(O.dequantize(np.zeros_like(w), one, b), np.repeat(b, 64, axis=1))
+
+
+def test_dequant_group_mapping():
+    n, k = 4, 512
+    w = O.pack_codes(np.ones((n, k), np.uint8))
+    s = O.f32_to_bf16_bits(2.0 ** -np.arange(k // 64, dtype=np.float32))[None, :].repeat(n, 0)
+    got = O.bf16_bits_to_f32(O.dequantize(w, s, np.zeros_like(s)))
+    for kk in range(k):
+        assert (got[:, kk] == 2.0 ** -(kk // 64)).all()
+
+
+@pytest.mark.parametrize("case", golden_io.qmm_cases(), ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
+def test_qmm_matches_bruteforce(case):
+    deq = O.dequantize(case["w"], case["s"], case["b"])
+    assert np.array_equal(deq, case["deq"])
+    exact = O.quantized_matmul_exact(case["x"], case["w"], case["s"], case["b"])
+    np.testing.assert_allclose(exact, case["exact"], rtol=1e-12, atol=1e-12)
+    y = O.quantized_matmul(case["x"], case["w"], case["s"], case["b"])
+    assert np.array_equal(y, case["y"])
+
+
+def test_qmm_one_hot_picks_weights():
+    x0, w, s, b = O.make_inputs(1, 256, 32, seed=5)
+    deq = O.bf16_bits_to_f32(O.dequantize(w, s, b))
+    for kk in (0, 7, 8, 63, 64, 200, 255):
+        x = np.zeros((1, 256), np.uint16)
+        x[0, kk] = 0x3F80  # 1.0
+        y = O.quantized_matmul_exact(x, w, s, b)
+        assert np.array_equal(y[0], deq[:, kk].astype(np.float64))
+
+
+def test_qmm_integer_codes():
+    rng = np.random.default_rng(6)
+    m, k, n = 5, 384, 48
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    xi = rng.integers(-8, 8, size=(m, k))
+    x = O.f32_to_bf16_bits(xi.astype(np.float32))
+    one = np.full((n, k // 64), 0x3F80, np.uint16)
+    y = O.quantized_matmul_exact(x, w, one, np.zeros_like(one))
+    assert np.array_equal(y, (xi @ bytes_view_codes(w).astype(np.int64).T).astype(np.float64))
+
+
+def test_qmm_linearity_and_pow2_scaling():
+    x, w, s, b = O.make_inputs(4, 256, 64, seed=7)
+    y = O.quantized_matmul_exact(x, w, s, b)
+    x2 = O.f32_to_bf16_bits(O.bf16_bits_to_f32(x) * 2)
+    assert np.array_equal(O.quantized_matmul_exact(x2, w, s, b), 2 * y)
+    xa, _, _, _ = O.make_inputs(4, 256, 64, seed=8)
+    xs = O.bf16_bits_to_f32(x).astype(np.float64) + O.bf16_bits_to_f32(xa)
+    wd = O.bf16_bits_to_f32(O.dequantize(w, s, b)).astype(np.float64)
+    np.testing.assert_allclose(y + O.quantized_matmul_exact(xa, w, s, b), xs @ wd.T, rtol=1e-12, atol=1e-12)
+
+
+def test_planted_mistakes_fail():
+    """A plausible mistake in the oracle must be caught by the pins above."""
+    case = golden_io.qmm_cases()[3]
+    # Reversed nibble order inside each word.
+    q = O.unpack_codes(case["w"]).reshape(case["n"], -1, 8)[:, :, ::-1].reshape(case["n"], -1)
+    assert not np.array_equal(O.dequantize(O.pack_codes(q), case["s"], case["b"]), case["deq"])
+    # Raw-code accumulation s*sum(qx) + b*sum(x), skipping the bf16 rounding of the weights: out
+    # of the mean-relative tolerance at a model-sized K.
+    x, w, s, b = O.make_inputs(16, 5120, 512, seed=0)
+    ref = O.quantized_matmul_exact(x, w, s, b)
+    q = O.unpack_codes(w).astype(np.float64)
+    raw = O.bf16_bits_to_f32(x).astype(np.float64) @ (q * np.repeat(O.bf16_bits_to_f32(s), 64, 1)
+                                                     + np.repeat(O.bf16_bits_to_f32(b), 64, 1)).T
+    raw_bf16 = O.bf16_bits_to_f32(O.f32_to_bf16_bits(raw.astype(np.float32)))
+    assert O.mean_rel(raw_bf16, ref) > O.MEAN_REL_TOL
+    good = O.bf16_bits_to_f32(O.quantized_matmul(x, w, s, b))
+    assert O.mean_rel(good, ref) < O.MEAN_REL_TOL and O.max_rel(good, ref) < O.MAX_REL_TOL
+
+
+def test_pack_nax_matches_index_loops():
+    z = golden_io.load("pack_nax.npz")
+    wq2, sp2, _ = O.pack_nax(z["w"], z["s"], z["s"])
+    assert np.array_equal(wq2, z["wq2"]) and np.array_equal(sp2, z["sp2"])
+    w, s, b = O.unpack_nax(wq2, sp2, sp2, z["w"].shape[0])
+    assert np.array_equal(w, z["w"]) and np.array_equal(s, z["s"]) and np.array_equal(b, z["s"])
+
+
+def test_metrics_closed_forms():
+    ref = np.array([1.0, -2.0, 4.0])
+    y = np.array([1.5, -2.0, 4.0])
+    assert O.max_rel(y, ref) == pytest.approx(0.5 / 4)
+    assert O.mean_rel(y, ref) == pytest.approx((0.5 / 3) / (7 / 3))
+    assert O.rel_l2(y, ref) == pytest.approx(0.5 / np.sqrt(21))
+
+
+def test_workload_bytes_and_flops():
+    # The workload table's byte counts: c0 15.07 MB, c1 100.35/100.43/100.59, c2 53.02, c3 447.63, c4 234.68.
+    expect = {(16, 5120, 5120): 15.07, (1, 5120, 34816): 100.35, (2, 5120, 34816): 100.43,
+              (4, 5120, 34816): 100.59, (64, 17408, 5120): 53.02, (32, 5120, 151936): 447.63,
+              (4096, 5120, 17408): 234.68}
+    for (m, k, n), mb in expect.items():
+        assert O.bytes_per_call(m, k, n) / 1e6 == pytest.approx(mb, abs=0.006)
+    assert O.flops_per_call(4096, 5120, 17408) / 1e9 == pytest.approx(730.14, abs=0.01)
+
+
+def test_make_inputs_deterministic_and_distributed():
+    a = O.make_inputs(4, 512, 64, seed=1)
+    b = O.make_inputs(4, 512, 64, seed=1)
+    for u, v in zip(a, b):
+        assert np.array_equal(u, v)
+    x, w, s, bb = O.make_inputs(8, 5120, 256, sigma=0.5, seed=2)
+    q = O.unpack_codes(w)
+    counts = np.bincount(q.ravel(), minlength=16) / q.size
+    assert np.abs(counts - 1 / 16).max() < 0.002
+    sf = O.bf16_bits_to_f32(s)
+    assert sf.min() >= 1e-4 * 0.99 and abs(O.bf16_bits_to_f32(x).std() - 0.5) < 0.01
+    bf = O.bf16_bits_to_f32(bb)
+    assert np.abs(bf + 8 * sf).max() < 0.01
+    x1, *_ = O.config_inputs(1, m=1)
+    x4, *_ = O.config_inputs(1)
+    assert x4.shape == (4, 5120) and np.array_equal(x1, x4[:1])
+
+
+def test_c_restatement_matches_numpy_oracle():
+    x, w, s, b = O.make_inputs(9, 1024, 96, seed=4)
+    assert np.array_equal(cpu.dequant(w, s, b), O.dequantize(w, s, b))
+    ref = O.quantized_matmul_exact(x, w, s, b)
+    y = O.bf16_bits_to_f32(cpu.qmm(x, w, s, b))
+    assert O.max_rel(y, ref) < O.MAX_REL_TOL and O.mean_rel(y, ref) < O.MEAN_REL_TOL
+    yf = cpu.qmm_f32(x, w, s, b)
+    np.testing.assert_allclose(yf, ref, rtol=1e-4, atol=1e-4 * np.abs(ref).max())
+    assert np.array_equal(O.f32_to_bf16_bits(yf), cpu.qmm(x, w, s, b))
+    w2, s2, b2, expected, _ = golden_io.dequant_table_weights()
+    assert np.array_equal(cpu.dequant(w2, s2, b2), expected)
