@@ -5,8 +5,8 @@ Bars:
     over every finite bf16 scale and random model-sized weights;
   * quantized_matmul: the north-star tolerance against the fp32-accumulated reference
     (max|y-ref|/max|ref| <= 1e-2, mean|y-ref|/mean|ref| <= 2e-3), and, much tighter, per element:
-    at least 99% of outputs equal bf16_rne(ref) and every other output is one bf16 ulp from it
-    (only the fp32 accumulation order differs from the oracle);
+    at least 99% of outputs equal bf16_rne(ref) and every other output is within one bf16 ulp of
+    ref plus 2^-17 * sum_k |x||w| (only the fp32 accumulation order differs from the oracle);
   * size-independent properties at the full workload sizes: determinism, y(2x) == 2 y(x).
 """
 
@@ -48,19 +48,42 @@ def gpu_qmm(x, w, s, b):
     return host_bits(y)
 
 
-def check_qmm(y_bits, ref, what=""):
+def abs_dot(x, w, s, b, rows, cols):
+    """S[i] = sum_k |x[rows[i], k]| * |dequant(w)[cols[i], k]|: the scale of fp32 rounding error
+    in output (rows[i], cols[i])."""
+    ucols, inv = np.unique(cols, return_inverse=True)
+    wd = np.abs(O.bf16_bits_to_f32(O.dequantize(w[ucols], s[ucols], b[ucols])).astype(np.float64))
+    xa = np.abs(O.bf16_bits_to_f32(x).astype(np.float64))
+    return np.einsum("ik,ik->i", xa[rows], wd[inv])
+
+
+def check_qmm(y_bits, ref, what="", inputs=None):
+    """North-star tolerances, plus per element: at least 99% of outputs equal bf16_rne(ref), and
+    every other one is within one bf16 ulp of ref plus 2^-17 * sum_k |x||w| (fp32 accumulation
+    in another order can move a result near zero by many of its own ulps, never by more)."""
     ref = np.asarray(ref, dtype=np.float64)
     y = O.bf16_bits_to_f32(y_bits).astype(np.float64)
     mx, mn = O.max_rel(y, ref), O.mean_rel(y, ref)
     rne = O.f32_to_bf16_bits(ref.astype(np.float32))
     mism = y_bits != rne
-    # Any other output must be a bf16 neighbour of bf16_rne(ref) (same sign, one ulp away).
-    step = np.abs(y_bits.astype(np.int32) - rne.astype(np.int32))
-    far = mism & ((step != 1) | ((y_bits >> 15) != (rne >> 15)))
-    note(f"  {what} max_rel={mx:.2e} mean_rel={mn:.2e} mismatches={int(mism.sum())}/{mism.size} far={int(far.sum())}")
+    nm = int(mism.sum())
+    far = 0
+    if nm and inputs is not None:
+        x, w, s, b = inputs
+        rows, cols = np.nonzero(mism.reshape(-1, mism.shape[-1]))
+        sel = np.arange(rows.size)
+        if sel.size > 4096:
+            sel = np.random.default_rng(0).choice(sel, 4096, replace=False)
+        rows, cols = rows[sel], cols[sel]
+        yy = y.reshape(-1, y.shape[-1])[rows, cols]
+        rr = ref.reshape(-1, ref.shape[-1])[rows, cols]
+        ulp = np.spacing(np.abs(O.bf16_bits_to_f32(rne.reshape(-1, rne.shape[-1])[rows, cols])).astype(np.float32)) * 65536.0
+        bound = ulp + 2.0 ** -17 * abs_dot(np.asarray(x).reshape(-1, np.asarray(x).shape[-1]), w, s, b, rows, cols)
+        far = int((np.abs(yy - rr) > bound).sum())
+    note(f"  {what} max_rel={mx:.2e} mean_rel={mn:.2e} mismatches={nm}/{mism.size} far={far}")
     assert mx <= O.MAX_REL_TOL and mn <= O.MEAN_REL_TOL
-    assert int(mism.sum()) <= max(2, mism.size // 100)
-    assert not far.any()
+    assert nm <= max(2, mism.size // 100)
+    assert far == 0
 
 
 def test_native_library_is_loaded():
@@ -108,7 +131,7 @@ def test_dequant_random(n, k):
                          ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
 def test_qmm_bruteforce_cases(case):
     y = gpu_qmm(case["x"], case["w"], case["s"], case["b"])
-    check_qmm(y, case["exact"], "golden")
+    check_qmm(y, case["exact"], "golden", (case["x"], case["w"], case["s"], case["b"]))
 
 
 ROWS = [1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 24, 31, 32, 33, 40, 47, 48, 63, 64]
@@ -117,14 +140,14 @@ ROWS = [1, 2, 3, 4, 5, 7, 8, 9, 15, 16, 17, 24, 31, 32, 33, 40, 47, 48, 63, 64]
 @pytest.mark.parametrize("m", ROWS)
 def test_qmm_skinny_rows(m):
     x, w, s, b = O.make_inputs(m, 512, 272, seed=m)  # N % 32 == 16: a half column tile
-    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"M={m}")
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"M={m}", (x, w, s, b))
 
 
 @pytest.mark.parametrize("m", [1, 4, 16, 32, 64])
 @pytest.mark.parametrize("k,n", [(128, 16), (5120, 1024), (17408, 256), (1024, 4112)])
 def test_qmm_skinny_shapes(m, k, n):
     x, w, s, b = O.make_inputs(m, k, n, seed=k + n + m)
-    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}")
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}", (x, w, s, b))
 
 
 @pytest.mark.parametrize("m", [64, 100, 2048])
@@ -135,14 +158,14 @@ def test_reference_prefill_kernel_shapes(m, k, n):
     x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=0)
     y = quantized_matmul(bf16_dev(x).reshape(1, m, k), u32_dev(w), bf16_dev(s), bf16_dev(b))
     assert tuple(y.shape) == (1, m, n)
-    check_qmm(host_bits(y).reshape(m, n), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}")
+    check_qmm(host_bits(y).reshape(m, n), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}", (x, w, s, b))
 
 
 @pytest.mark.parametrize("m,k,n", [(65, 5120, 1024), (255, 128, 528), (256, 256, 256), (257, 1024, 784),
                                    (1024, 5120, 1040), (4096, 1024, 512)])
 def test_qmm_gemm_shapes(m, k, n):
     x, w, s, b = O.make_inputs(m, k, n, seed=m + k)
-    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}")
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}", (x, w, s, b))
 
 
 # ----------------------------------------------------------------------------- workloads
@@ -155,7 +178,7 @@ def test_workload_full(index, m):
     note(f"workload {index} M={m}")
     x, w, s, b = O.config_inputs(index, m=m)
     y = gpu_qmm(x, w, s, b)
-    check_qmm(y, workload_ref(x, w, s, b), f"c{index} M={m}")
+    check_qmm(y, workload_ref(x, w, s, b), f"c{index} M={m}", (x, w, s, b))
 
 
 def test_workload_prefill_sampled_rows():
@@ -164,7 +187,7 @@ def test_workload_prefill_sampled_rows():
     y = gpu_qmm(x, w, s, b)
     rows = np.random.default_rng(4).choice(x.shape[0], 256, replace=False)
     rows.sort()
-    check_qmm(y[rows], workload_ref(x[rows], w, s, b), "c4 sampled rows")
+    check_qmm(y[rows], workload_ref(x[rows], w, s, b), "c4 sampled rows", (x[rows], w, s, b))
 
 
 @pytest.mark.parametrize("index,m", [(0, 16), (1, 4), (2, 64), (3, 32), (4, 4096)])
@@ -184,11 +207,11 @@ def test_side_stream_and_workspace_growth():
     side = torch.cuda.Stream()
     for x, w, s, b in cases + cases[::-1]:
         ref = O.quantized_matmul_exact(x, w, s, b)
-        check_qmm(gpu_qmm(x, w, s, b), ref, "default stream")
+        check_qmm(gpu_qmm(x, w, s, b), ref, "default stream", (x, w, s, b))
         with torch.cuda.stream(side):
             y = quantized_matmul(bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b))
         side.synchronize()
-        check_qmm(host_bits(y), ref, "side stream")
+        check_qmm(host_bits(y), ref, "side stream", (x, w, s, b))
 
 
 def test_noncontiguous_and_empty():
@@ -196,7 +219,7 @@ def test_noncontiguous_and_empty():
     xbig = bf16_dev(np.concatenate([x, x], axis=1))
     xv = xbig[:, 256:]  # non-contiguous view
     y = quantized_matmul(xv, u32_dev(w), bf16_dev(s), bf16_dev(b))
-    check_qmm(host_bits(y), O.quantized_matmul_exact(x, w, s, b), "strided x")
+    check_qmm(host_bits(y), O.quantized_matmul_exact(x, w, s, b), "strided x", (x, w, s, b))
     y0 = quantized_matmul(bf16_dev(x[:0]), u32_dev(w), bf16_dev(s), bf16_dev(b))
     assert tuple(y0.shape) == (0, 64)
 
