@@ -42,7 +42,7 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // Per-device facts, queried once.
 struct DeviceInfo {
   int cus = 0;
-  int occ[3] = {0, 0, 0};  // resident skinny workgroups per CU, per variant
+  int occ[5] = {0, 0, 0, 0, 0};  // resident skinny workgroups per CU, per variant
 };
 
 // Split-K workspace for one (device, stream): [counters | partials]. Counters are zeroed when the
@@ -63,7 +63,7 @@ int device_info(int dev, DeviceInfo** out) {
     DeviceInfo d;
     hipError_t e = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
-    for (int v = 0; v < 3; ++v) d.occ[v] = qmm4::skinny_occupancy(v);
+    for (int v = 0; v < 5; ++v) d.occ[v] = qmm4::skinny_occupancy(v);
     it = g_dev.emplace(dev, d).first;
   }
   *out = &it->second;
@@ -168,7 +168,11 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   plan.variant = qmm4::skinny_variant_for_rows((int)M, &plan.tile_cols);
   plan.tiles = (int)((N + plan.tile_cols - 1) / plan.tile_cols);
   plan.units = (long long)plan.tiles * (K / 128);
+  // One resident workgroup per slot, but at least 4 units each: a tile split over fewer units
+  // per workgroup costs more in fp32 partials than it gains in balance.
   long long slots = (long long)di->cus * di->occ[plan.variant];
+  const long long cap = std::max(1LL, plan.units / 4);
+  if (slots > cap) slots = cap;
   if (slots < 1) slots = 1;
   plan.blocks = (int)(plan.units < slots ? plan.units : slots);
 

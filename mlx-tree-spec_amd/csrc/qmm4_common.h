@@ -20,6 +20,15 @@ typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 constexpr int kGroup = 64;  // quantization group along K
 
+// Word 3 of a raw (stride 0) buffer resource on gfx9 CDNA: 32-bit data format, no swizzle.
+constexpr int kBufferRsrcWord3 = 0x00020000;
+
+// num_records of a buffer resource holding `bytes` bytes (the field is an unsigned 32-bit count;
+// callers keep every buffer below 4 GiB).
+__device__ __forceinline__ int rsrc_bytes(unsigned long long bytes) {
+  return (int)(uint32_t)(bytes < 0xFFFFFFFFull ? bytes : 0xFFFFFFFFull);
+}
+
 __device__ __forceinline__ float bf16_to_f32(uint32_t bits16) { return __uint_as_float(bits16 << 16); }
 
 // Two fp32 values -> two bf16 (round to nearest even) in one dword, `a` in the low half.
@@ -56,6 +65,37 @@ __device__ __forceinline__ u32x4 dequant_word(uint32_t w, float s, float s16, fl
   r.w = pack_bf16x2(__builtin_fmaf(q6, s, b), __builtin_fmaf(h7, s16, b));
   return r;
 }
+
+// Faster exact dequantization of one word: 17 VALU instead of 22 (1 shift, 4 AND, 8 v_fma_mix_f32,
+// 4 cvt_pk).
+//
+// Each AND leaves two codes in the low mantissa bits of the two fp16 halves of a dword, where they
+// read as fp16 subnormals: q * 2^-24 (code at bits 0-3 of a byte) or 16q * 2^-24 (bits 4-7).
+// v_fma_mix_f32 widens an fp16 half to fp32 exactly (fp16 subnormals are preserved: the kernels
+// run with denormal mode 3) and computes, with one rounding,
+//     fma(q * 2^-24,   s * 2^24, b) = s*q + b
+//     fma(16q * 2^-24, s * 2^20, b) = s*q + b
+// so the result is fp32_rne(s*q + b), bit-identical to dequant_word, whenever s * 2^24 is finite
+// (|s| < 2^104, see fast_scale_ok). s24 = s * 2^24 and s20 = s * 2^20 are exact multiplications.
+__device__ __forceinline__ u32x4 dequant_word_fast(uint32_t w, float s24, float s20, float b) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  const uint32_t w8 = w >> 8;
+  const h2 d0 = __builtin_bit_cast(h2, w & 0x000F000Fu);   // k0, k4
+  const h2 d1 = __builtin_bit_cast(h2, w & 0x00F000F0u);   // k1, k5 (x16)
+  const h2 d2 = __builtin_bit_cast(h2, w8 & 0x000F000Fu);  // k2, k6
+  const h2 d3 = __builtin_bit_cast(h2, w8 & 0x00F000F0u);  // k3, k7 (x16)
+  u32x4 r;
+  r.x = pack_bf16x2(__builtin_fmaf((float)d0.x, s24, b), __builtin_fmaf((float)d1.x, s20, b));
+  r.y = pack_bf16x2(__builtin_fmaf((float)d2.x, s24, b), __builtin_fmaf((float)d3.x, s20, b));
+  r.z = pack_bf16x2(__builtin_fmaf((float)d0.y, s24, b), __builtin_fmaf((float)d1.y, s20, b));
+  r.w = pack_bf16x2(__builtin_fmaf((float)d2.y, s24, b), __builtin_fmaf((float)d3.y, s20, b));
+  return r;
+}
+
+// dequant_word_fast is exact for a bf16 scale with exponent field <= 230 (|s| < 2^104, so s * 2^24
+// is finite): every finite scale of practical size, zero and subnormal included. Larger and
+// non-finite scales take dequant_word.
+__device__ __forceinline__ bool fast_scale_ok(uint32_t sbits) { return (sbits & 0x7F80u) <= (230u << 7); }
 
 __device__ __forceinline__ bf16x8 as_bf16x8(u32x4 v) { return __builtin_bit_cast(bf16x8, v); }
 

@@ -126,6 +126,59 @@ def test_dequant_random(n, k):
     assert np.array_equal(got, O.dequantize(w, s, b))
 
 
+# ----------------------------------------------------------------------------- dequant inside qmm
+def scale_bias_pairs(kind, n, rng):
+    """bf16 (s, b) bit patterns for n groups. 'fast': scale exponent field in [0, 230], the
+    range the kernels dequantize with v_fma_mix_f32 (zero and subnormal scales included), with
+    biases of any exponent up to 60 fields away; 'slow': scales in [2^104, 2^124), which the kernels
+    send to the general form; 'mixed': one group in eight slow. Every dequantized value is finite."""
+    def bits(sign, e, m):
+        return ((sign << 15) | (e << 7) | m).astype(np.uint16)
+    sgn = lambda: rng.integers(0, 2, n, dtype=np.uint32)
+    man = lambda: rng.integers(0, 128, n, dtype=np.uint32)
+    if kind in ("fast", "slow"):
+        lo, hi = (0, 231) if kind == "fast" else (231, 251)
+        es = rng.integers(lo, hi, n, dtype=np.uint32)
+        es[:2] = [lo, hi - 1]
+        eb = np.clip(es.astype(np.int64) + rng.integers(-60, 61, n), 0, 250).astype(np.uint32)
+        s, b = bits(sgn(), es, man()), bits(sgn(), eb, man())
+        if kind == "fast":
+            s[2], b[3] = 0, 0  # a zero scale, a zero bias
+        return s, b
+    sf, bf = scale_bias_pairs("fast", n, rng)
+    sl, bl = scale_bias_pairs("slow", n, rng)
+    pick = rng.integers(0, 8, n) == 0
+    return np.where(pick, sl, sf), np.where(pick, bl, bf)
+
+
+@pytest.mark.parametrize("kind", ["fast", "slow", "mixed"])
+@pytest.mark.parametrize("m", [64, 32, 4])
+def test_qmm_one_hot_is_exact_dequant(kind, m):
+    """y = x @ dequant(w).T with one-hot rows of x reads single dequantized weights, so the
+    dequantization inside the matmul kernels must equal the oracle's bit for bit (zeros of
+    either sign compare equal: the fp32 sum turns -0 into +0)."""
+    n, k = 4096, 256
+    rng = np.random.default_rng({"fast": 1, "slow": 2, "mixed": 3}[kind] * 100 + m)
+    s, b = scale_bias_pairs(kind, n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    deq = O.dequantize(w, s, b)
+    dv = O.bf16_bits_to_f32(deq)
+    assert np.isfinite(dv).all()
+    # Subnormal bf16 weights would test the MFMA's handling of subnormals, not the dequant.
+    sub = (deq & 0x7F80) == 0
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in range(0, k, m):
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), k0 + np.arange(m)] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = deq[:, k0:k0 + m].T
+        yv, rv = O.bf16_bits_to_f32(y), O.bf16_bits_to_f32(ref)
+        keep = ~sub[:, k0:k0 + m].T
+        bad = keep & (yv != rv)
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 # ----------------------------------------------------------------------------- small / golden
 @pytest.mark.parametrize("case", [c for c in golden_io.qmm_cases() if c["k"] % 128 == 0 and c["n"] % 16 == 0],
                          ids=lambda c: f"{c['m']}x{c['k']}x{c['n']}")
