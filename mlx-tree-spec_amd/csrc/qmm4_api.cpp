@@ -42,7 +42,7 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 // Per-device facts, queried once.
 struct DeviceInfo {
   int cus = 0;
-  int occ[5] = {0, 0, 0, 0, 0};  // resident skinny workgroups per CU, per variant
+  int occ[qmm4::kSkinnyVariants] = {};  // resident skinny workgroups per CU, per variant
 };
 
 // Split-K workspace for one (device, stream): [counters | partials]. Counters are zeroed when the
@@ -63,7 +63,7 @@ int device_info(int dev, DeviceInfo** out) {
     DeviceInfo d;
     hipError_t e = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
-    for (int v = 0; v < 5; ++v) d.occ[v] = qmm4::skinny_occupancy(v);
+    for (int v = 0; v < qmm4::kSkinnyVariants; ++v) d.occ[v] = qmm4::skinny_occupancy(v);
     it = g_dev.emplace(dev, d).first;
   }
   *out = &it->second;
@@ -141,8 +141,10 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   if (!x || !w || !scales || !biases || !y) return fail(QMM4_ERR_INVALID, "null pointer argument");
   if (!aligned(x, 16) || !aligned(w, 16))
     return fail(QMM4_ERR_INVALID, "x and w must be 16-byte aligned");
-  if (!aligned(scales, 2) || !aligned(biases, 2) || !aligned(y, 2))
-    return fail(QMM4_ERR_INVALID, "scales, biases and y must be 2-byte aligned");
+  if (!aligned(scales, 4) || !aligned(biases, 4) || !aligned(y, 2))
+    return fail(QMM4_ERR_INVALID, "scales and biases must be 4-byte aligned and y 2-byte aligned");
+  if ((unsigned long long)N * (unsigned long long)K / 2 >= (1ULL << 32))
+    return fail(QMM4_ERR_INVALID, "w of %lld x %lld codes exceeds 4 GiB", (long long)N, (long long)K);
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
   const uint16_t* xb = static_cast<const uint16_t*>(x);
@@ -164,14 +166,19 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   rc = device_info(dev, &di);
   if (rc) return rc;
 
+  // A unit spans V super-steps; V must divide K / 128, and a unit's 2V scales (biases) of a row
+  // are read with one 4V-byte load, so the scale and bias pointers must be 4V-byte aligned.
+  int vmax = 4;
+  const long long ks = K / 128;
+  while (vmax > 1 && (ks % vmax != 0 || !aligned(scales, 4 * vmax) || !aligned(biases, 4 * vmax))) vmax >>= 1;
   qmm4::SkinnyPlan plan;
-  plan.variant = qmm4::skinny_variant_for_rows((int)M, &plan.tile_cols);
+  plan.variant = qmm4::skinny_variant((int)M, vmax, &plan.tile_cols, &plan.steps_v);
   plan.tiles = (int)((N + plan.tile_cols - 1) / plan.tile_cols);
-  plan.units = (long long)plan.tiles * (K / 128);
-  // One resident workgroup per slot, but at least 4 units each: a tile split over fewer units
+  plan.units = (long long)plan.tiles * (ks / plan.steps_v);
+  // One resident workgroup per slot, but at least 2 units each: a tile split over fewer units
   // per workgroup costs more in fp32 partials than it gains in balance.
   long long slots = (long long)di->cus * di->occ[plan.variant];
-  const long long cap = std::max(1LL, plan.units / 4);
+  const long long cap = std::max(1LL, plan.units / 2);
   if (slots > cap) slots = cap;
   if (slots < 1) slots = 1;
   plan.blocks = (int)(plan.units < slots ? plan.units : slots);

@@ -7,17 +7,19 @@
 
 namespace qmm4 {
 
-// Skinny (M <= 64) stream-K kernel geometry, chosen by M.
+// Skinny (M <= 64) stream-K kernel geometry, chosen by M, K and the scale/bias alignment.
 struct SkinnyPlan {
-  int variant;   // index into the kernel table (see qmm4_skinny.hip)
-  int tile_cols; // output columns per tile (CW)
-  int blocks;    // workgroups launched (G)
-  int tiles;     // tiles along N (T)
-  long long units;  // T * (K / 128)
+  int variant;      // index into the kernel table (see qmm4_skinny.hip)
+  int tile_cols;    // output columns per tile (CW)
+  int steps_v;      // super-steps (128 k) per unit (V)
+  int blocks;       // workgroups launched (G)
+  int tiles;        // tiles along N (T)
+  long long units;  // T * K / (128 * V)
 };
 
-// Returns the variant for M rows (1..64) and its columns per tile.
-int skinny_variant_for_rows(int M, int* tile_cols);
+constexpr int kSkinnyVariants = 12;
+// Variant for M rows when a unit may span up to `vmax` super-steps (1, 2 or 4).
+int skinny_variant(int M, int vmax, int* tile_cols, int* steps_v);
 // Resident workgroups per CU for a variant (from the HIP occupancy API; cached by the caller).
 int skinny_occupancy(int variant);
 // Enqueue the skinny kernel. `part` holds blocks*2*M*tile_cols floats, `cnt` tiles zeroed uint32s.
