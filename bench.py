@@ -142,6 +142,25 @@ def cpu_baseline(wl_rows, k, n, budget_s: float = 10.0) -> dict:
             "ms_per_step": round(el / steps * 1e3, 2)}
 
 
+def profile_mode(torch, lib, dev, args) -> int:
+    """Launches only, for counter collection: the workload's steps, then a copy of known size whose
+    FETCH_SIZE / WRITE_SIZE calibrate the counters against bytes that are certainly moved once."""
+    wl = Workload(args.profile, torch, lib, dev)
+    for _ in range(args.steps):
+        wl.step()
+    torch.cuda.synchronize()
+    n = (args.copy_mib << 20) // 4
+    src = torch.empty(n, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(7)
+    for _ in range(5):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    log(f"[bench] profile {args.profile}: {args.steps} steps of M={list(wl.rows)}, "
+        f"5 copies of {args.copy_mib} MiB; done")
+    return 0
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -151,6 +170,10 @@ def main() -> int:
     ap.add_argument("--samples", type=int, default=30, help="single-launch samples per workload")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--profile", default=None, metavar="WORKLOAD",
+                    help="launch-only mode for rocprofv3: run WORKLOAD's steps --steps times, then a plain "
+                         "device-to-device copy of --copy-mib MiB five times (counter calibration); no timing")
+    ap.add_argument("--copy-mib", type=int, default=512)
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -168,6 +191,8 @@ def main() -> int:
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = _lib.load()
+    if args.profile:
+        return profile_mode(torch, lib, dev, args)
     only = [s.strip() for s in args.only.split(",") if s.strip()]
     if "c1" not in only:
         only = ["c1"] + only
@@ -229,10 +254,14 @@ def main() -> int:
         byts.append(bytes_per_call(m, wl.k, wl.n))
     achieved = sum(byts) / sum(durs) / 1e9
     traffic = None
-    tpath = os.path.join(ROOT, "profiles", "traffic_decode_gate_up.json")
+    # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE and
+    # WRITE_SIZE passes (scaled by a copy of known size); null when that summary is absent.
+    tpath = os.path.join(ROOT, "profiles", "skinny_decode_gate_up_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
-            traffic = json.load(f).get("hbm_bytes_per_launch")
+            for ln in f:
+                if ln.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(float(ln.split(":", 1)[1]))
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -244,7 +273,7 @@ def main() -> int:
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qmm4::skinny_kernel (M<=16 variant)",
+                     "kernel": "qmm4::skinny_kernel<qmm4::SkinnyCfg<4, 4, 1, 2, 4>> (rows <= 4)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
                      "bytes_per_launch": round(statistics.mean(byts))},
         "workloads": out_workloads,

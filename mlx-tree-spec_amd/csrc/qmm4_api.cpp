@@ -176,8 +176,12 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   plan.tiles = (int)((N + plan.tile_cols - 1) / plan.tile_cols);
   plan.units = (long long)plan.tiles * (ks / plan.steps_v);
   // One resident workgroup per slot, but at least 2 units each: a tile split over fewer units
-  // per workgroup costs more in fp32 partials than it gains in balance.
-  long long slots = (long long)di->cus * di->occ[plan.variant];
+  // per workgroup costs more in fp32 partials than it gains in balance. Three workgroups per CU
+  // (12 waves) measured faster than four on every skinny shape from M=1 to M=64.
+#ifndef QMM4_SKINNY_MAX_WG_PER_CU
+#define QMM4_SKINNY_MAX_WG_PER_CU 3
+#endif
+  long long slots = (long long)di->cus * std::min(di->occ[plan.variant], QMM4_SKINNY_MAX_WG_PER_CU);
   const long long cap = std::max(1LL, plan.units / 2);
   if (slots > cap) slots = cap;
   if (slots < 1) slots = 1;

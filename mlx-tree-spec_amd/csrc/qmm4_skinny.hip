@@ -34,6 +34,10 @@
 #include "qmm4_common.h"
 #include "qmm4_kernels.h"
 
+#ifndef QMM4_SKINNY_W_AUX
+#define QMM4_SKINNY_W_AUX 0
+#endif
+
 namespace qmm4 {
 
 struct SkinnyParams {
@@ -340,21 +344,32 @@ void skinny_kernel(SkinnyParams P) {
   load_x<C>(xr, P.x, P.M, P.K, st0);
 
   // Weight prefetch ring, PF steps ahead; (tp, sp) is the next unit to fetch, fi its index.
-  // Fetches are unconditional (past the range's end they repeat its last unit) so that the ring
-  // stays in fixed registers and the compiler waits only for the slot being consumed.
+  // Fetches are unconditional so that the ring stays in fixed registers and the compiler waits
+  // only for the slot being consumed. Past the range's end they go through zero-length buffer
+  // resources: out-of-range buffer loads return zeros without a memory access (re-reading the
+  // last unit instead would miss the L2 and cost up to PF units of HBM traffic per workgroup).
+  const int wrec = rsrc_bytes((unsigned long long)P.N * (P.K >> 1));
+  const int srec = rsrc_bytes((unsigned long long)P.N * KG * 2);
   u32x4 wv[PF][CT][V];
   SB<V> sv[PF][CT], bv[PF][CT];
   uint32_t wo[CT], so[CT];
   int tp = t0, sp = st0, fi = 0;
   col_offsets<C>(P, L, tp, wo, so);
   auto fetch = [&](int j) {
+    const bool live = fi < nunits;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(P.w), 0, live ? wrec : 0, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.s), 0, live ? srec : 0, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.b), 0, live ? srec : 0, kBufferRsrcWord3);
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
 #pragma unroll
       for (int v = 0; v < V; ++v)
-        wv[j][ct][v] = __builtin_amdgcn_raw_buffer_load_b128(L.rw, wo[ct] + v * 64, sp * V * 64, 0);
-      sv[j][ct] = load_sb<V>(L.rs, so[ct], sp * 4 * V);
-      bv[j][ct] = load_sb<V>(L.rb, so[ct], sp * 4 * V);
+        wv[j][ct][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[ct] + v * 64, sp * V * 64, QMM4_SKINNY_W_AUX);
+      sv[j][ct] = load_sb<V>(rs, so[ct], sp * 4 * V);
+      bv[j][ct] = load_sb<V>(rb, so[ct], sp * 4 * V);
     }
     if (++fi < nunits) {
       if (++sp == NS) {
@@ -504,10 +519,13 @@ void skinny_kernel(SkinnyParams P) {
 // Kernel table: id -> (rows, V, CT, PF, waves per SIMD). The x slice of a step is at most 16 KB
 // (rows * V <= 64), so larger row counts take shorter steps; V = 2 and 1 also serve K that four
 // super-steps do not divide.
+#ifndef QMM4_SKINNY_PF_SMALL
+#define QMM4_SKINNY_PF_SMALL 2  // prefetch depth of the variants for up to 16 rows
+#endif
 #define QMM4_SKINNY_VARIANTS(X) \
-  X(0, 4, 4, 1, 2, 4)           \
-  X(1, 8, 4, 1, 2, 4)           \
-  X(2, 16, 4, 1, 2, 4)          \
+  X(0, 4, 4, 1, QMM4_SKINNY_PF_SMALL, 4) \
+  X(1, 8, 4, 1, QMM4_SKINNY_PF_SMALL, 4) \
+  X(2, 16, 4, 1, QMM4_SKINNY_PF_SMALL, 4) \
   X(3, 32, 2, 1, 2, 4)          \
   X(4, 64, 1, 1, 2, 4)          \
   X(5, 4, 2, 1, 2, 4)           \
