@@ -127,7 +127,7 @@ def cpu_baseline(wl_rows, k, n, budget_s: float = 10.0) -> dict:
             cpu.qmm(x[:m], w, s, b)
         steps += 1
         el = time.perf_counter() - t0
-        if el >= budget_s or steps >= 200:
+        if el >= budget_s or steps >= 5000:
             break
     total = steps * sum(bytes_per_call(m, k, n) for m in wl_rows)
     model = ""
@@ -273,7 +273,7 @@ def main() -> int:
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qmm4::skinny_kernel<qmm4::SkinnyCfg<4, 4, 1, 2, 4>> (rows <= 4)",
+                     "kernel": "qmm4::skinny_kernel<qmm4::SkinnyCfg<4, 4, 1, 2, 4, 12>> (rows <= 4, resident x)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
                      "bytes_per_launch": round(statistics.mean(byts))},
         "workloads": out_workloads,

@@ -181,11 +181,29 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
 #ifndef QMM4_SKINNY_MAX_WG_PER_CU
 #define QMM4_SKINNY_MAX_WG_PER_CU 3
 #endif
-  long long slots = (long long)di->cus * std::min(di->occ[plan.variant], QMM4_SKINNY_MAX_WG_PER_CU);
-  const long long cap = std::max(1LL, plan.units / 2);
-  if (slots > cap) slots = cap;
-  if (slots < 1) slots = 1;
-  plan.blocks = (int)(plan.units < slots ? plan.units : slots);
+  auto blocks_for = [&](int variant) {
+    long long slots = (long long)di->cus * std::min(di->occ[variant], QMM4_SKINNY_MAX_WG_PER_CU);
+    const long long cap = std::max(1LL, plan.units / 2);
+    if (slots > cap) slots = cap;
+    if (slots < 1) slots = 1;
+    return (int)(plan.units < slots ? plan.units : slots);
+  };
+  plan.blocks = blocks_for(plan.variant);
+#ifndef QMM4_SKINNY_NO_RESIDENT_X
+  // Resident x when every workgroup's range fits the twin's x slots: a range of u units touches
+  // min(u, steps per tile) distinct steps, and no range holds more than ceil(units / blocks) units.
+  int xslots = 0;
+  const int twin = qmm4::skinny_resident_twin(plan.variant, &xslots);
+  if (twin >= 0) {
+    const int tb = blocks_for(twin);
+    const long long per_wg = (plan.units + tb - 1) / tb;
+    const long long ns = ks / plan.steps_v;
+    if (std::min(per_wg, ns) <= xslots) {
+      plan.variant = twin;
+      plan.blocks = tb;
+    }
+  }
+#endif
 
   uint32_t* cnt = nullptr;
   float* part = nullptr;

@@ -17,9 +17,13 @@ struct SkinnyPlan {
   long long units;  // T * K / (128 * V)
 };
 
-constexpr int kSkinnyVariants = 12;
+constexpr int kSkinnyVariants = 15;
 // Variant for M rows when a unit may span up to `vmax` super-steps (1, 2 or 4).
 int skinny_variant(int M, int vmax, int* tile_cols, int* steps_v);
+// The resident-x twin of a variant (same geometry; x staged once per workgroup) and its number of
+// x slots: a launch may use it only if no workgroup's range touches more distinct steps than
+// that. -1 when the variant has none.
+int skinny_resident_twin(int variant, int* slots);
 // Resident workgroups per CU for a variant (from the HIP occupancy API; cached by the caller).
 int skinny_occupancy(int variant);
 // Enqueue the skinny kernel. `part` holds blocks*2*M*tile_cols floats, `cnt` tiles zeroed uint32s.

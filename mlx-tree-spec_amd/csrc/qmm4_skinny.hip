@@ -25,18 +25,17 @@
 //    neighbouring workgroups: their fp32 partials are stored with device-coherent stores, and
 //    after the whole range has streamed the workgroup counts in on their counters; the last
 //    contributor sums the partials in contributor order (deterministic).
-//  * x: the step's slice x[0:M, k-range] is staged in LDS (double-buffered, one barrier per
-//    step), already in A-fragment order with only the M real rows; the next step's slice is
-//    loaded into registers before that step's weight prefetches are issued, so waiting for it
-//    never waits for weights still in flight (the vector memory counter is in order).
+//  * x: staged in LDS in A-fragment order with only the M real rows. Resident form (M <= 16 when
+//    the range touches few enough steps): the slices of all the range's steps are staged once,
+//    behind the first weight prefetches, and the stream has no barrier but the one closing each
+//    tile. Staged form: each step's slice is staged as the step begins (double-buffered, one
+//    barrier per step); the next step's slice is loaded into registers before that step's weight
+//    prefetches are issued, so waiting for it never waits for weights still in flight (the vector
+//    memory counter is in order).
 #include <type_traits>
 
 #include "qmm4_common.h"
 #include "qmm4_kernels.h"
-
-#ifndef QMM4_SKINNY_W_AUX
-#define QMM4_SKINNY_W_AUX 0
-#endif
 
 namespace qmm4 {
 
@@ -54,7 +53,7 @@ struct SkinnyParams {
   long long U;    // units = T * NS
 };
 
-template <int MP_, int V_, int CT_, int PF_, int WPE_>
+template <int MP_, int V_, int CT_, int PF_, int WPE_, int XS_>
 struct SkinnyCfg {
   static constexpr int MP = MP_;               // rows served (M <= MP), a power of two
   static constexpr int MB = (MP + 15) / 16;    // 16-row MFMA blocks
@@ -68,7 +67,19 @@ struct SkinnyCfg {
   static constexpr int XU = MP * V * 16;       // 16-byte units of a step's x slice
   static constexpr int kXR = (XU + kThreads - 1) / kThreads;  // x-staging registers per thread
   static constexpr int LGV = V == 4 ? 2 : V == 2 ? 1 : 0;
+  // Resident x: 0 = each step's x slice is staged in LDS as the step begins (double-buffered, one
+  // barrier per step); XS > 0 = the x slices of every step the workgroup's range touches (at most
+  // XS distinct steps) are staged once before the stream starts, and the stream has no barriers
+  // but the one closing each tile.
+  static constexpr int XS = XS_;
+  static constexpr int kXSlots = XS > 0 ? XS : 2;
 };
+
+// LDS slot of step st when the range begins at step st0 (resident x).
+__device__ __forceinline__ int x_slot(int st, int st0, int NS) {
+  const int sl = st - st0;
+  return sl < 0 ? sl + NS : sl;
+}
 
 // The 2V scales (or biases) of one row for one step: V dwords, loaded with one buffer load.
 template <int V>
@@ -223,7 +234,7 @@ __device__ __forceinline__ void col_offsets(const SkinnyParams& P, const LaneCtx
 // path for tiles that hold a scale outside dequant_word_fast's range.
 template <class C>
 __device__ __forceinline__ void redo_segment(const SkinnyParams& P, const LaneCtx& L, int t, int a, int e,
-                                             u32x4* xs, f32x4 (&acc)[C::MB][C::CT]) {
+                                             u32x4 (*xs)[C::XU], int st0, f32x4 (&acc)[C::MB][C::CT]) {
   constexpr int MB = C::MB, CT = C::CT, V = C::V;
   uint32_t wo[CT], so[CT];
   col_offsets<C>(P, L, t, wo, so);
@@ -232,10 +243,16 @@ __device__ __forceinline__ void redo_segment(const SkinnyParams& P, const LaneCt
   for (int rb = 0; rb < MB; ++rb) aoff[rb] = L.g * 4 * C::MP + min(rb * 16 + L.n, P.M - 1);
   u32x4 xr[C::kXR];
   for (int st = a; st < e; ++st) {
-    __syncthreads();
-    load_x<C>(xr, P.x, P.M, P.K, st);
-    store_x<C>(xs, xr, P.M);
-    __syncthreads();
+    u32x4* xb;
+    if constexpr (C::XS > 0) {
+      xb = xs[x_slot(st, st0, P.NS)];
+    } else {
+      __syncthreads();
+      load_x<C>(xr, P.x, P.M, P.K, st);
+      store_x<C>(xs[0], xr, P.M);
+      __syncthreads();
+      xb = xs[0];
+    }
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
       const SB<V> sv = load_sb<V>(L.rs, so[ct], st * 4 * V);
@@ -252,7 +269,7 @@ __device__ __forceinline__ void redo_segment(const SkinnyParams& P, const LaneCt
 #pragma unroll
           for (int rb = 0; rb < MB; ++rb)
             acc[rb][ct] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(
-                as_bf16x8(xs[(v * 16 + tt) * C::MP + aoff[rb]]), as_bf16x8(B), acc[rb][ct], 0, 0, 0);
+                as_bf16x8(xb[(v * 16 + tt) * C::MP + aoff[rb]]), as_bf16x8(B), acc[rb][ct], 0, 0, 0);
         }
       }
     }
@@ -266,7 +283,7 @@ __global__ __launch_bounds__(C::kThreads) __attribute__((amdgpu_waves_per_eu(C::
 void skinny_kernel(SkinnyParams P) {
   constexpr int MB = C::MB, CT = C::CT, CW = C::CW, PF = C::PF, V = C::V;
   constexpr int kMaxRedo = 32;
-  __shared__ u32x4 xs[2][C::XU];
+  __shared__ u32x4 xs[C::kXSlots][C::XU];
   __shared__ int s_last[2];
   __shared__ int s_nredo;
   __shared__ int s_redo[kMaxRedo][3];
@@ -339,9 +356,9 @@ void skinny_kernel(SkinnyParams P) {
 #pragma unroll
   for (int rb = 0; rb < MB; ++rb) aoff[rb] = L.g * 4 * C::MP + min(rb * 16 + L.n, P.M - 1);
 
-  // x for the first step, into registers.
+  // x for the first step, into registers (staged x).
   u32x4 xr[C::kXR];
-  load_x<C>(xr, P.x, P.M, P.K, st0);
+  if constexpr (C::XS == 0) load_x<C>(xr, P.x, P.M, P.K, st0);
 
   // Weight prefetch ring, PF steps ahead; (tp, sp) is the next unit to fetch, fi its index.
   // Fetches are unconditional so that the ring stays in fixed registers and the compiler waits
@@ -367,7 +384,7 @@ void skinny_kernel(SkinnyParams P) {
     for (int ct = 0; ct < CT; ++ct) {
 #pragma unroll
       for (int v = 0; v < V; ++v)
-        wv[j][ct][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[ct] + v * 64, sp * V * 64, QMM4_SKINNY_W_AUX);
+        wv[j][ct][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[ct] + v * 64, sp * V * 64, 0);
       sv[j][ct] = load_sb<V>(rs, so[ct], sp * 4 * V);
       bv[j][ct] = load_sb<V>(rb, so[ct], sp * 4 * V);
     }
@@ -381,6 +398,22 @@ void skinny_kernel(SkinnyParams P) {
   };
 #pragma unroll
   for (int j = 0; j < PF; ++j) fetch(j);
+
+  if constexpr (C::XS > 0) {
+    // Resident x: stage the slices of the range's steps (st0, st0 + 1, ... wrapping at NS; at most
+    // XS of them, as the launch guarantees) behind the first weight prefetches.
+    const int nsl = nunits < NS ? nunits : NS;
+    for (int i = tid; i < nsl * C::XU; i += C::kThreads) {
+      const int sl = i / C::XU, it = i & (C::XU - 1);
+      int stp = st0 + sl;
+      if (stp >= NS) stp -= NS;
+      const int m = it >> (C::LGV + 4), v = (it >> 4) & (C::V - 1), q = it & 15;
+      if (m < P.M)
+        xs[sl][(v * 16 + q) * C::MP + m] = *reinterpret_cast<const u32x4*>(
+            P.x + (size_t)m * P.K + (size_t)(stp * V + v) * 128 + q * 8);
+    }
+    __syncthreads();
+  }
 
   f32x4 acc[MB][CT];
 #pragma unroll
@@ -396,10 +429,15 @@ void skinny_kernel(SkinnyParams P) {
     constexpr int j = decltype(jc)::value;
     // Publish this step's x (double-buffered: the barrier also tells that every wave is done
     // with step i-2, the previous user of this buffer), then fetch the next step's x.
-    u32x4* xb = xs[i & 1];
-    store_x<C>(xb, xr, P.M);
-    __syncthreads();
-    load_x<C>(xr, P.x, P.M, P.K, (st + 1 < NS) ? st + 1 : 0);
+    u32x4* xb;
+    if constexpr (C::XS > 0) {
+      xb = xs[x_slot(st, st0, NS)];
+    } else {
+      xb = xs[i & 1];
+      store_x<C>(xb, xr, P.M);
+      __syncthreads();
+      load_x<C>(xr, P.x, P.M, P.K, (st + 1 < NS) ? st + 1 : 0);
+    }
 
 #pragma unroll
     for (int ct = 0; ct < CT; ++ct) {
@@ -480,7 +518,7 @@ void skinny_kernel(SkinnyParams P) {
       for (int rb = 0; rb < MB; ++rb)
 #pragma unroll
         for (int ct = 0; ct < CT; ++ct) acc[rb][ct] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      redo_segment<C>(P, L, rt, ra, re, xs[0], acc);
+      redo_segment<C>(P, L, rt, ra, re, xs, st0, acc);
       store_tile(rt, acc);
     }
   }
@@ -516,27 +554,34 @@ void skinny_kernel(SkinnyParams P) {
   }
 }
 
-// Kernel table: id -> (rows, V, CT, PF, waves per SIMD). The x slice of a step is at most 16 KB
-// (rows * V <= 64), so larger row counts take shorter steps; V = 2 and 1 also serve K that four
-// super-steps do not divide.
+// Kernel table: id -> (rows, V, CT, PF, waves per SIMD, resident x slots). The x slice of a step
+// is at most 16 KB (rows * V <= 64), so larger row counts take shorter steps; V = 2 and 1 also
+// serve K that four super-steps do not divide. Variants 12-14 are the resident-x twins of 0-2
+// (48 KB of x slots each, three workgroups per CU).
 #ifndef QMM4_SKINNY_PF_SMALL
 #define QMM4_SKINNY_PF_SMALL 2  // prefetch depth of the variants for up to 16 rows
 #endif
+#ifndef QMM4_SKINNY_PF_RX
+#define QMM4_SKINNY_PF_RX 2     // prefetch depth of the resident-x variants
+#endif
 #define QMM4_SKINNY_VARIANTS(X) \
-  X(0, 4, 4, 1, QMM4_SKINNY_PF_SMALL, 4) \
-  X(1, 8, 4, 1, QMM4_SKINNY_PF_SMALL, 4) \
-  X(2, 16, 4, 1, QMM4_SKINNY_PF_SMALL, 4) \
-  X(3, 32, 2, 1, 2, 4)          \
-  X(4, 64, 1, 1, 2, 4)          \
-  X(5, 4, 2, 1, 2, 4)           \
-  X(6, 8, 2, 1, 2, 4)           \
-  X(7, 16, 2, 1, 2, 4)          \
-  X(8, 4, 1, 1, 2, 4)           \
-  X(9, 8, 1, 1, 2, 4)           \
-  X(10, 16, 1, 1, 2, 4)         \
-  X(11, 32, 1, 1, 2, 4)
+  X(0, 4, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0)   \
+  X(1, 8, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0)   \
+  X(2, 16, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0)  \
+  X(3, 32, 2, 1, 2, 4, 0)                     \
+  X(4, 64, 1, 1, 2, 4, 0)                     \
+  X(5, 4, 2, 1, 2, 4, 0)                      \
+  X(6, 8, 2, 1, 2, 4, 0)                      \
+  X(7, 16, 2, 1, 2, 4, 0)                     \
+  X(8, 4, 1, 1, 2, 4, 0)                      \
+  X(9, 8, 1, 1, 2, 4, 0)                      \
+  X(10, 16, 1, 1, 2, 4, 0)                    \
+  X(11, 32, 1, 1, 2, 4, 0)                    \
+  X(12, 4, 4, 1, QMM4_SKINNY_PF_RX, 4, 12)    \
+  X(13, 8, 4, 1, QMM4_SKINNY_PF_RX, 4, 6)     \
+  X(14, 16, 4, 1, QMM4_SKINNY_PF_RX, 4, 3)
 
-#define QMM4_CFG_TYPE(id, mp, v, ct, pf, wpe) typedef SkinnyCfg<mp, v, ct, pf, wpe> SkCfg##id;
+#define QMM4_CFG_TYPE(id, mp, v, ct, pf, wpe, xs) typedef SkinnyCfg<mp, v, ct, pf, wpe, xs> SkCfg##id;
 QMM4_SKINNY_VARIANTS(QMM4_CFG_TYPE)
 #undef QMM4_CFG_TYPE
 
@@ -554,9 +599,18 @@ int skinny_variant(int M, int vmax, int* tile_cols, int* steps_v) {
   return id;
 }
 
+int skinny_resident_twin(int variant, int* slots) {
+  switch (variant) {
+    case 0: *slots = SkCfg12::XS; return 12;
+    case 1: *slots = SkCfg13::XS; return 13;
+    case 2: *slots = SkCfg14::XS; return 14;
+    default: *slots = 0; return -1;
+  }
+}
+
 static const void* skinny_func(int variant) {
   switch (variant) {
-#define QMM4_FUNC(id, mp, v, ct, pf, wpe) \
+#define QMM4_FUNC(id, mp, v, ct, pf, wpe, xs) \
   case id: return reinterpret_cast<const void*>(&skinny_kernel<SkCfg##id>);
     QMM4_SKINNY_VARIANTS(QMM4_FUNC)
 #undef QMM4_FUNC
@@ -579,7 +633,7 @@ hipError_t launch_skinny(const SkinnyPlan& plan, const uint16_t* x, const uint32
   P.M = M; P.N = N; P.K = K; P.NS = K / (128 * plan.steps_v); P.G = plan.blocks; P.U = plan.units;
   const dim3 grid((unsigned)plan.blocks), block(256);
   switch (plan.variant) {
-#define QMM4_LAUNCH(id, mp, v, ct, pf, wpe) \
+#define QMM4_LAUNCH(id, mp, v, ct, pf, wpe, xs) \
   case id: hipLaunchKernelGGL(skinny_kernel<SkCfg##id>, grid, block, 0, stream, P); break;
     QMM4_SKINNY_VARIANTS(QMM4_LAUNCH)
 #undef QMM4_LAUNCH
