@@ -89,10 +89,12 @@ int get_workspace(int dev, hipStream_t stream, size_t counter_bytes, size_t part
       return fail(QMM4_ERR_NOMEM, "workspace allocation of %zu bytes failed: %s", cb + pb,
                   hipGetErrorString(e));
     }
-    e = hipMemsetAsync(p, 0, cb, stream);
+    // Counters start at zero (each launch leaves them at zero). Cleared by a kernel rather than
+    // hipMemsetAsync, which misbehaves when recorded into a captured graph.
+    e = qmm4::launch_zero_u32(static_cast<uint32_t*>(p), cb / sizeof(uint32_t), stream);
     if (e != hipSuccess) {
       (void)hipFree(p);
-      return hip_fail(e, "hipMemsetAsync(workspace counters)");
+      return hip_fail(e, "workspace counter clear");
     }
     ws.base = p;
     ws.counter_bytes = cb;

@@ -31,6 +31,9 @@ hipError_t launch_skinny(const SkinnyPlan& plan, const uint16_t* x, const uint32
                          const uint16_t* s, const uint16_t* b, uint16_t* y, float* part,
                          uint32_t* cnt, int M, int N, int K, hipStream_t stream);
 
+// Zero n uint32 words (the skinny kernel's arrival counters when their workspace is allocated).
+hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
+
 // LDS-tiled MFMA GEMM for M > 64.
 hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s,
                        const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream);

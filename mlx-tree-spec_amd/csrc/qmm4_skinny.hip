@@ -32,6 +32,7 @@
 //    barrier per step); the next step's slice is loaded into registers before that step's weight
 //    prefetches are issued, so waiting for it never waits for weights still in flight (the vector
 //    memory counter is in order).
+#include <algorithm>
 #include <type_traits>
 
 #include "qmm4_common.h"
@@ -597,6 +598,17 @@ int skinny_variant(int M, int vmax, int* tile_cols, int* steps_v) {
   *tile_cols = 64;  // every variant: 4 waves x 1 column block x 16 columns
   *steps_v = v;
   return id;
+}
+
+__global__ __launch_bounds__(256) void zero_u32_kernel(uint32_t* __restrict__ p, size_t n) {
+  for (size_t i = (size_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (size_t)gridDim.x * 256) p[i] = 0u;
+}
+
+hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream) {
+  if (n == 0) return hipSuccess;
+  const size_t blocks = std::min<size_t>((n + 255) / 256, 1024);
+  hipLaunchKernelGGL(zero_u32_kernel, dim3((unsigned)blocks), dim3(256), 0, stream, p, n);
+  return hipGetLastError();
 }
 
 int skinny_resident_twin(int variant, int* slots) {
