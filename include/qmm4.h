@@ -41,7 +41,8 @@ extern "C" {
  *   x: bf16 [M, K]; w: uint32 [N, K/8]; scales, biases: bf16 [N, K/group_size]; y: bf16 [M, N].
  *   Requires M >= 0, N % 16 == 0, K % 128 == 0 (the reference's packed path requires K % 128 == 0,
  *   packed_linear.py:57), group_size == 64, bits == 4, transpose == 1, each of M, N, K <= 2^30,
- *   w smaller than 4 GiB (N * K / 2 < 2^32 bytes), x and w 16-byte aligned, scales and biases
+ *   w, x and y each below 4 GiB (with 256 rows of margin: (N + 256) * K / 2, (M + 256) * K * 2 and
+ *   (M + 256) * N * 2 bytes below 2^32), x and w 16-byte aligned, scales and biases
  *   4-byte aligned, y 2-byte aligned. M == 0 or N == 0 is a no-op. Rows M <= 64 run the skinny
  *   HBM-bound kernel, larger M the MFMA GEMM; the choice is a fixed function of the shape and the
  *   scale/bias alignment. Results are deterministic (bit-identical across calls and streams).

@@ -145,8 +145,14 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
     return fail(QMM4_ERR_INVALID, "x and w must be 16-byte aligned");
   if (!aligned(scales, 4) || !aligned(biases, 4) || !aligned(y, 2))
     return fail(QMM4_ERR_INVALID, "scales and biases must be 4-byte aligned and y 2-byte aligned");
-  if ((unsigned long long)N * (unsigned long long)K / 2 >= (1ULL << 32))
+  // Kernels address w, x and y with 32-bit byte offsets (tiles may reach 256 rows or columns past
+  // the end, which read as zero / are dropped), so each stays below 4 GiB with that margin.
+  if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 32))
     return fail(QMM4_ERR_INVALID, "w of %lld x %lld codes exceeds 4 GiB", (long long)N, (long long)K);
+  if ((unsigned long long)(M + 256) * (unsigned long long)K * 2 >= (1ULL << 32) ||
+      (unsigned long long)(M + 256) * (unsigned long long)N * 2 >= (1ULL << 32))
+    return fail(QMM4_ERR_INVALID, "x [%lld, %lld] or y [%lld, %lld] exceeds 4 GiB", (long long)M,
+                (long long)K, (long long)M, (long long)N);
 
   hipStream_t stream = static_cast<hipStream_t>(hip_stream);
   const uint16_t* xb = static_cast<const uint16_t*>(x);

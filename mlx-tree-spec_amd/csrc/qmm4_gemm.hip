@@ -8,9 +8,19 @@
 // Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 4 waves in a 2 x 2
 // arrangement, each wave a 128 x 128 block of 4 x 4 MFMA 32x32x16 tiles (256 fp32 accumulators
 // per lane). LDS holds two stages of [256][64 + 8] bf16 for the activations and for the
-// dequantized weights (147 KB); the next stage is prefetched into registers during the MFMAs of
-// the current one. Workgroup ids are remapped so that consecutive tiles land on one XCD and tiles
-// are walked in groups of 4 row tiles, so a group shares weight and activation blocks in L2.
+// dequantized weights (147 KB).
+//
+// Pipeline (one wave per SIMD, so each wave hides its own latencies): the raw inputs of a K step
+// (activation chunks, packed codes, scale and bias) are loaded into registers two steps ahead of
+// their use, through buffer resources (rows past M and columns past N read as zero). While the
+// MFMAs of step kt run from LDS stage kt % 2, the same wave writes step kt + 1 into the other
+// stage: activations as loaded, weights dequantized exactly in registers (dequant_word_fast; a
+// thread whose group has a scale outside its range rewrites its column with dequant_word after the
+// MFMAs). One barrier per step. Workgroup ids are remapped so that consecutive tiles land on one
+// XCD and tiles are walked in groups of 4 row tiles, so a group shares weight and activation
+// blocks in L2. The output tile is staged through LDS and stored as 16-byte row chunks.
+#include <type_traits>
+
 #include "qmm4_common.h"
 #include "qmm4_kernels.h"
 
@@ -18,7 +28,8 @@ namespace qmm4 {
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;  // LDS row pitch in bf16
+constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;  // LDS row pitch (bf16) of a K step
+constexpr int LDC = BN + 8;                                // LDS row pitch (bf16) of the output tile
 constexpr int kThreads = 256;
 constexpr int kGroupM = 4;
 
@@ -30,6 +41,13 @@ struct GemmParams {
   uint16_t* y;
   int M, N, K;
   int tiles_m, tiles_n;
+};
+
+// One K step's raw inputs held by a thread.
+struct Raw {
+  u32x4 a[8];      // activations: rows a_r0 + 32 j of the tile, 16-byte chunk a_kc of the step
+  u32x4 w[2];      // the 8 code words (one group) of column n0 + tid
+  uint32_t s, b;   // that group's scale and bias (bf16 bits)
 };
 
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
@@ -54,55 +72,57 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int tm = first_m + in_group % gm;
   const int tn = in_group / gm;
   const int m0 = tm * BM, n0 = tn * BN;
+  const int nk = P.K / BK;  // even: K % 128 == 0
 
-  const size_t KW = (size_t)(P.K >> 3), KG = (size_t)(P.K >> 6);
-  const int nk = P.K / BK;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(P.w), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 1)), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.s), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
 
-  // Loader roles. Activations: thread owns 16-B chunk (tid & 7) of rows (tid >> 3) + 32*j.
+  // Loader roles. Activations: 16-byte chunk a_kc of rows a_r0 + 32 j. Weights: column n0 + tid.
   const int a_kc = tid & 7;
   const int a_r0 = tid >> 3;
-  // Weights: thread owns column n0 + tid, the 8 words (one group) of each K step.
-  const int bn_col = n0 + tid;
-  const bool b_ok = bn_col < P.N;
-  const uint32_t* wrow = P.w + (b_ok ? (size_t)bn_col : 0) * KW;
-  const uint16_t* srow = P.s + (b_ok ? (size_t)bn_col : 0) * KG;
-  const uint16_t* brow = P.b + (b_ok ? (size_t)bn_col : 0) * KG;
+  const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
+  const uint32_t xrow32 = 32u * (uint32_t)P.K * 2u;
+  const uint32_t col = (uint32_t)(n0 + tid);
+  const uint32_t woff = col * (uint32_t)(P.K >> 1);
+  const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
 
-  u32x4 ra[8];
-  u32x4 rw[2];
-  uint32_t rs = 0, rbias = 0;
-
-  auto load_stage = [&](int kt) {
-    const int k0 = kt * BK;
+  Raw raw[2];
+  // Steps past the last are clamped to it (their data is written to an LDS stage nobody reads).
+  auto load = [&](int kt, Raw& R) {
+    const int k = kt < nk ? kt : nk - 1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int r = m0 + a_r0 + 32 * j;
-      if (r < P.M)
-        ra[j] = *reinterpret_cast<const u32x4*>(P.x + (size_t)r * P.K + k0 + a_kc * 8);
-      else
-        ra[j] = u32x4{0u, 0u, 0u, 0u};
-    }
-    if (b_ok) {
-      rw[0] = *reinterpret_cast<const u32x4*>(wrow + (size_t)kt * 8);
-      rw[1] = *reinterpret_cast<const u32x4*>(wrow + (size_t)kt * 8 + 4);
-      rs = srow[kt];
-      rbias = brow[kt];
-    } else {
-      rw[0] = rw[1] = u32x4{0u, 0u, 0u, 0u};
-      rs = rbias = 0;
-    }
+    for (int j = 0; j < 8; ++j)
+      R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff + (uint32_t)j * xrow32, k * BK * 2, 0);
+    R.w[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff, k * 32, 0);
+    R.w[1] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff + 16u, k * 32, 0);
+    R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
+    R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
   };
-
-  auto store_stage = [&](int st) {
-    uint16_t* as = As + st * BM * LDK;
+  auto store_a = [&](const Raw& R, int st, int j0, int j1) {
+    uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<u32x4*>(as + (a_r0 + 32 * j) * LDK + a_kc * 8) = ra[j];
+    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + 32 * j * LDK) = R.a[j];
+  };
+  auto store_b_fast = [&](const Raw& R, int st, int j0, int j1) {
     uint16_t* bs = Bs + st * BN * LDK + tid * LDK;
-    const float sf = bf16_to_f32(rs), bf = bf16_to_f32(rbias), s16 = sf * 0.0625f;
+    const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
+    const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
+#pragma unroll
+    for (int j = j0; j < j1; ++j)
+      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j >> 2][j & 3], s24, s20, bf);
+  };
+  auto store_b_exact = [&](const Raw& R, int st) {
+    uint16_t* bs = Bs + st * BN * LDK + tid * LDK;
+    const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
 #pragma unroll
     for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(rw[j >> 2][j & 3], sf, s16, bf);
+      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
   };
 
   f32x16 acc[4][4];
@@ -113,17 +133,16 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
-  load_stage(0);
-  store_stage(0);
-  __syncthreads();
-
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * 8;
-  for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
-    if (kt + 1 < nk) load_stage(kt + 1);
-    const uint16_t* as = As + st * BM * LDK + (wm * 128 + lrow) * LDK + lk;
-    const uint16_t* bs = Bs + st * BN * LDK + (wn * 128 + lrow) * LDK + lk;
+
+  // Step kt: MFMAs from LDS stage kt % 2 while step kt + 1 (raw[(kt + 1) % 2]) is written into the
+  // other stage; then step kt + 3 is loaded into the registers just written out.
+  auto step = [&](int kt, auto parity) {
+    constexpr int ST = decltype(parity)::value;
+    Raw& R = raw[ST ^ 1];
+    const uint16_t* as = As + ST * BM * LDK + (wm * 128 + lrow) * LDK + lk;
+    const uint16_t* bs = Bs + ST * BN * LDK + (wn * 128 + lrow) * LDK + lk;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
       bf16x8 Af[4], Bf[4];
@@ -137,24 +156,58 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
       for (int i = 0; i < 4; ++i)
 #pragma unroll
         for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<32>::mma(Af[i], Bf[j], acc[i][j]);
+      if (ks == 0) store_a(R, ST ^ 1, 0, 4);
+      if (ks == 1) store_a(R, ST ^ 1, 4, 8);
+      if (ks == 2) store_b_fast(R, ST ^ 1, 0, 4);
+      if (ks == 3) store_b_fast(R, ST ^ 1, 4, 8);
     }
-    if (kt + 1 < nk) store_stage(st ^ 1);
+    if (!fast_scale_ok(R.s)) store_b_exact(R, ST ^ 1);
     __syncthreads();
+    load(kt + 3, R);
+  };
+
+  // Prologue: steps 0 and 1 in registers, step 0 in LDS, step 2 in flight.
+  load(0, raw[0]);
+  load(1, raw[1]);
+  store_a(raw[0], 0, 0, 8);
+  store_b_fast(raw[0], 0, 0, 8);
+  if (!fast_scale_ok(raw[0].s)) store_b_exact(raw[0], 0);
+  load(2, raw[0]);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; kt += 2) {
+    step(kt, std::integral_constant<int, 0>{});
+    step(kt + 1, std::integral_constant<int, 1>{});
   }
 
-  // Epilogue: fp32 -> bf16, row-guarded for the M tail and column-guarded for the N tail.
+  // Epilogue: the 256 x 256 tile as bf16 through LDS (every wave is past the last step's reads),
+  // then 16-byte row chunks; rows past M fall outside y's buffer resource, columns past N are skipped
+  // (N % 16 == 0, so a chunk is entirely inside or outside).
+  uint16_t* Cs = smem;
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
-      const int n = n0 + wn * 128 + j * 32 + lrow;
-      if (n >= P.N) continue;
+      const int n = wn * 128 + j * 32 + lrow;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = m0 + wm * 128 + i * 32 + Mfma<32>::row(lane, r);
-        if (m < P.M) P.y[(size_t)m * P.N + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
+        const int m = wm * 128 + i * 32 + Mfma<32>::row(lane, r);
+        Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
       }
     }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+#pragma unroll 4
+  for (int q = 0; q < BM * BN / 8 / kThreads; ++q) {
+    const int c = tid + q * kThreads;
+    const int r = c >> 5, ch = c & 31;
+    const int gn = n0 + ch * 8;
+    if (gn < P.N) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
+      __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)(m0 + r) * (uint32_t)P.N + (uint32_t)gn) * 2u, 0, 0);
+    }
+  }
 }
 
 constexpr size_t kSmemBytes = (size_t)2 * (BM + BN) * LDK * sizeof(uint16_t);
