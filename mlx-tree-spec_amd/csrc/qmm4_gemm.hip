@@ -5,20 +5,21 @@
 // BN x BK block is dequantized once to bf16 (qmm_packed.py:629-637) into LDS and multiplied with
 // the BM x BK activation block; accumulation in fp32; bf16 out.
 //
-// Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 4 waves in a 2 x 2
-// arrangement, each wave a 128 x 128 block of 4 x 4 MFMA 32x32x16 tiles (256 fp32 accumulators
-// per lane). LDS holds two stages of [256][64 + 8] bf16 for the activations and for the
-// dequantized weights (147 KB).
+// Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 8 waves in a 2 x 4
+// arrangement (two waves per SIMD, so one wave's loads and LDS traffic overlap the other's MFMAs),
+// each wave a 128 x 64 block of 4 x 2 MFMA 32x32x16 tiles (128 fp32 accumulators per lane). LDS
+// holds two stages of [256][64 + 8] bf16 for the activations and for the dequantized weights
+// (147 KB).
 //
-// Pipeline (one wave per SIMD, so each wave hides its own latencies): the raw inputs of a K step
-// (activation chunks, packed codes, scale and bias) are loaded into registers two steps ahead of
-// their use, through buffer resources (rows past M and columns past N read as zero). While the
-// MFMAs of step kt run from LDS stage kt % 2, the same wave writes step kt + 1 into the other
-// stage: activations as loaded, weights dequantized exactly in registers (dequant_word_fast; a
-// thread whose group has a scale outside its range rewrites its column with dequant_word after the
-// MFMAs). One barrier per step. Workgroup ids are remapped so that consecutive tiles land on one
-// XCD and tiles are walked in groups of 4 row tiles, so a group shares weight and activation
-// blocks in L2. The output tile is staged through LDS and stored as 16-byte row chunks.
+// Pipeline: the raw inputs of a K step (activation chunks, packed codes, scale and bias) are loaded
+// into registers two steps ahead of their use, through buffer resources (rows past M and columns
+// past N read as zero). While the MFMAs of step kt run from LDS stage kt % 2, the wave writes step
+// kt + 1 into the other stage: activations as loaded, weights dequantized exactly in registers
+// (dequant_word_fast; a thread whose group has a scale outside its range rewrites its words with
+// dequant_word after the MFMAs). One barrier per step. Workgroup ids are remapped so that
+// consecutive tiles land on one XCD and tiles are walked in groups of 4 row tiles, so a group
+// shares weight and activation blocks in L2. The output tile is staged through LDS and stored as
+// 16-byte row chunks.
 #include <type_traits>
 
 #include "qmm4_common.h"
@@ -30,7 +31,7 @@ namespace {
 
 constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;  // LDS row pitch (bf16) of a K step
 constexpr int LDC = BN + 8;                                // LDS row pitch (bf16) of the output tile
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;
 constexpr int kGroupM = 4;
 
 struct GemmParams {
@@ -45,8 +46,8 @@ struct GemmParams {
 
 // One K step's raw inputs held by a thread.
 struct Raw {
-  u32x4 a[8];      // activations: rows a_r0 + 32 j of the tile, 16-byte chunk a_kc of the step
-  u32x4 w[2];      // the 8 code words (one group) of column n0 + tid
+  u32x4 a[4];      // activations: rows a_r0 + 64 j of the tile, 16-byte chunk a_kc of the step
+  u32x4 w;         // code words 4 * b_half .. 4 * b_half + 3 of column n0 + b_col (half a group)
   uint32_t s, b;   // that group's scale and bias (bf16 bits)
 };
 
@@ -58,7 +59,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 1, wn = wave & 1;
+  const int wm = wave >> 2, wn = wave & 3;
 
   // Tile id: XCD-contiguous remap, then grouped row-major walk.
   const int G = gridDim.x;
@@ -83,13 +84,15 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
 
-  // Loader roles. Activations: 16-byte chunk a_kc of rows a_r0 + 32 j. Weights: column n0 + tid.
+  // Loader roles. Activations: 16-byte chunk a_kc of rows a_r0 + 64 j (row j's offset goes in the
+  // scalar offset). Weights: words 4 * b_half .. + 3 of column n0 + b_col.
   const int a_kc = tid & 7;
   const int a_r0 = tid >> 3;
   const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
-  const uint32_t xrow32 = 32u * (uint32_t)P.K * 2u;
-  const uint32_t col = (uint32_t)(n0 + tid);
-  const uint32_t woff = col * (uint32_t)(P.K >> 1);
+  const int xrow64 = 64 * P.K * 2;
+  const int b_col = tid >> 1, b_half = tid & 1;
+  const uint32_t col = (uint32_t)(n0 + b_col);
+  const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)b_half * 16u;
   const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
 
   Raw raw[2];
@@ -97,39 +100,38 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   auto load = [&](int kt, Raw& R) {
     const int k = kt < nk ? kt : nk - 1;
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff + (uint32_t)j * xrow32, k * BK * 2, 0);
-    R.w[0] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff, k * 32, 0);
-    R.w[1] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff + 16u, k * 32, 0);
+    for (int j = 0; j < 4; ++j)
+      R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrow64, 0);
+    R.w = __builtin_amdgcn_raw_buffer_load_b128(rw, woff, k * 32, 0);
     R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
     R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
   };
   auto store_a = [&](const Raw& R, int st, int j0, int j1) {
     uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
 #pragma unroll
-    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + 32 * j * LDK) = R.a[j];
+    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + 64 * j * LDK) = R.a[j];
   };
   auto store_b_fast = [&](const Raw& R, int st, int j0, int j1) {
-    uint16_t* bs = Bs + st * BN * LDK + tid * LDK;
+    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_half * 32;
     const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
     const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
 #pragma unroll
     for (int j = j0; j < j1; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j >> 2][j & 3], s24, s20, bf);
+      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j], s24, s20, bf);
   };
   auto store_b_exact = [&](const Raw& R, int st) {
-    uint16_t* bs = Bs + st * BN * LDK + tid * LDK;
+    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_half * 32;
     const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
+    for (int j = 0; j < 4; ++j)
+      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j], sf, sf * 0.0625f, bf);
   };
 
-  f32x16 acc[4][4];
+  f32x16 acc[4][2];
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < 2; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -142,35 +144,38 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
     constexpr int ST = decltype(parity)::value;
     Raw& R = raw[ST ^ 1];
     const uint16_t* as = As + ST * BM * LDK + (wm * 128 + lrow) * LDK + lk;
-    const uint16_t* bs = Bs + ST * BN * LDK + (wn * 128 + lrow) * LDK + lk;
+    const uint16_t* bs = Bs + ST * BN * LDK + (wn * 64 + lrow) * LDK + lk;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 Af[4], Bf[4];
+      bf16x8 Af[4], Bf[2];
 #pragma unroll
       for (int i = 0; i < 4; ++i)
         Af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
 #pragma unroll
-      for (int j = 0; j < 4; ++j)
+      for (int j = 0; j < 2; ++j)
         Bf[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
 #pragma unroll
       for (int i = 0; i < 4; ++i)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) acc[i][j] = Mfma<32>::mma(Af[i], Bf[j], acc[i][j]);
-      if (ks == 0) store_a(R, ST ^ 1, 0, 4);
-      if (ks == 1) store_a(R, ST ^ 1, 4, 8);
-      if (ks == 2) store_b_fast(R, ST ^ 1, 0, 4);
-      if (ks == 3) store_b_fast(R, ST ^ 1, 4, 8);
+        for (int j = 0; j < 2; ++j) acc[i][j] = Mfma<32>::mma(Af[i], Bf[j], acc[i][j]);
+      if (ks == 0) store_a(R, ST ^ 1, 0, 2);
+      if (ks == 1) store_a(R, ST ^ 1, 2, 4);
+      if (ks == 2) store_b_fast(R, ST ^ 1, 0, 2);
+      if (ks == 3) store_b_fast(R, ST ^ 1, 2, 4);
     }
     if (!fast_scale_ok(R.s)) store_b_exact(R, ST ^ 1);
     __syncthreads();
     load(kt + 3, R);
+    // Keep these loads right behind the barrier (the scheduler would sink them toward their use two
+    // steps later, into the middle of the next step's MFMAs).
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // Prologue: steps 0 and 1 in registers, step 0 in LDS, step 2 in flight.
   load(0, raw[0]);
   load(1, raw[1]);
-  store_a(raw[0], 0, 0, 8);
-  store_b_fast(raw[0], 0, 0, 8);
+  store_a(raw[0], 0, 0, 4);
+  store_b_fast(raw[0], 0, 0, 4);
   if (!fast_scale_ok(raw[0].s)) store_b_exact(raw[0], 0);
   load(2, raw[0]);
   __syncthreads();
@@ -187,8 +192,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
 #pragma unroll
   for (int i = 0; i < 4; ++i)
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int n = wn * 128 + j * 32 + lrow;
+    for (int j = 0; j < 2; ++j) {
+      const int n = wn * 64 + j * 32 + lrow;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int m = wm * 128 + i * 32 + Mfma<32>::row(lane, r);
@@ -211,6 +216,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
 }
 
 constexpr size_t kSmemBytes = (size_t)2 * (BM + BN) * LDK * sizeof(uint16_t);
+static_assert((size_t)BM * LDC * sizeof(uint16_t) <= kSmemBytes, "output tile fits the K-step stages");
 
 }  // namespace
 
