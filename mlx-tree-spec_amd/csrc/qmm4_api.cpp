@@ -174,6 +174,16 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   rc = device_info(dev, &di);
   if (rc) return rc;
 
+#ifndef QMM4_NO_ROWSPLIT
+  // Up to 4 rows and enough output columns to give every CU its own rows: the row-split kernel.
+  qmm4::RowSplitPlan rplan;
+  if (qmm4::rowsplit_plan((int)M, (int)N, (int)K, di->cus, &rplan)) {
+    e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
+    if (e != hipSuccess) return hip_fail(e, "row-split kernel launch");
+    return QMM4_OK;
+  }
+#endif
+
   // A unit spans V super-steps; V must divide K / 128, and a unit's 2V scales (biases) of a row
   // are read with one 4V-byte load, so the scale and bias pointers must be 4V-byte aligned.
   int vmax = 4;

@@ -31,6 +31,20 @@ hipError_t launch_skinny(const SkinnyPlan& plan, const uint16_t* x, const uint32
                          const uint16_t* s, const uint16_t* b, uint16_t* y, float* part,
                          uint32_t* cnt, int M, int N, int K, hipStream_t stream);
 
+// Row-split decode kernel (up to 4 rows, output columns split evenly over one workgroup per CU).
+struct RowSplitPlan {
+  int V;        // super-steps (128 k) per unit
+  int R;        // weight rows per workgroup
+  int RB;       // 16-row blocks per workgroup
+  int IPW;      // super-steps per wave range
+  int blocks;   // workgroups
+  size_t smem;  // dynamic LDS bytes
+};
+// Fills `plan` and returns true when the shape suits the row-split kernel on `cus` CUs.
+bool rowsplit_plan(int M, int N, int K, int cus, RowSplitPlan* plan);
+hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                           const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream);
+
 // Zero n uint32 words (the skinny kernel's arrival counters when their workspace is allocated).
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 

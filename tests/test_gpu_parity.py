@@ -254,6 +254,42 @@ def test_workload_deterministic_and_pow2_linear(index, m):
     assert np.array_equal(O.bf16_bits_to_f32(y2x), 2 * O.bf16_bits_to_f32(y1))
 
 
+# ----------------------------------------------------------------------------- row-split path
+# Up to 4 rows with enough output columns to give every CU its own rows take the row-split
+# kernel (one workgroup per CU owning whole weight rows). N = 34816 + 32 leaves the last
+# workgroup a partial range and a half row block; K = 4096 gives units of 4 super-steps, 5120 of 5.
+@pytest.mark.parametrize("m,k,n", [(1, 5120, 34848), (3, 4096, 34816), (4, 5120, 34816), (2, 4096, 34848)])
+def test_rowsplit_shapes(m, k, n):
+    note(f"row-split {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 7 + k + n)
+    check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"row-split {m}x{k}x{n}", (x, w, s, b))
+
+
+@pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
+def test_rowsplit_one_hot_is_exact_dequant(kind):
+    """One-hot rows of x on the row-split path: each output is one dequantized weight and must
+    equal the oracle's bit for bit, for units dequantized in the fast form, in the general form
+    ('slow'), and for a mix of the two."""
+    n, k, m = 34848, 5120, 4
+    rng = np.random.default_rng({"fast": 11, "mixed": 12, "slow": 13}[kind])
+    s, b = scale_bias_pairs(kind, n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in (0, 1276, 5116):
+        ks = k0 + np.arange(m)
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), ks] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.empty((m, n), dtype=np.uint16)
+        for i, kk in enumerate(ks):
+            g = kk // 64
+            ref[i] = O.dequantize(w[:, 8 * g:8 * g + 8], s[:, g:g + 1], b[:, g:g + 1])[:, kk - 64 * g]
+        keep = (ref & 0x7F80) != 0  # subnormal bf16 weights test the MFMA, not the dequant
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 # ----------------------------------------------------------------------------- host integration
 def test_side_stream_and_workspace_growth():
     cases = [O.make_inputs(16, 5120, 512, seed=1), O.make_inputs(64, 17408, 1024, seed=2), O.make_inputs(3, 256, 64, seed=3)]
