@@ -160,12 +160,6 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   const uint16_t* bb = static_cast<const uint16_t*>(biases);
   uint16_t* yb = static_cast<uint16_t*>(y);
 
-  if (M > 64) {
-    hipError_t e = qmm4::launch_gemm(xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
-    if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
-    return QMM4_OK;
-  }
-
   int dev = 0;
   hipError_t e = hipGetDevice(&dev);
   if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
@@ -173,6 +167,12 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   DeviceInfo* di = nullptr;
   rc = device_info(dev, &di);
   if (rc) return rc;
+
+  if (M > 64) {
+    e = qmm4::launch_gemm(xb, w, sb, bb, yb, (int)M, (int)N, (int)K, di->cus, stream);
+    if (e != hipSuccess) return hip_fail(e, "gemm kernel launch");
+    return QMM4_OK;
+  }
 
 #ifndef QMM4_NO_ROWSPLIT
   // Up to 4 rows and enough output columns to give every CU its own rows: the row-split kernel.

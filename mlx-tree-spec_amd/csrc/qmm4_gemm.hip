@@ -29,10 +29,10 @@ namespace qmm4 {
 
 namespace {
 
-constexpr int BM = 256, BN = 256, BK = 64, LDK = BK + 8;  // LDS row pitch (bf16) of a K step
-constexpr int LDC = BN + 8;                                // LDS row pitch (bf16) of the output tile
+constexpr int BK = 64, LDK = BK + 8;  // K step; LDS row pitch (bf16) of a K step
 constexpr int kThreads = 512;
 constexpr int kGroupM = 4;
+constexpr int kTile = 256;            // the grid's tile; tail launches cut a tile into 128 x 128 quarters
 
 struct GemmParams {
   const uint16_t* x;
@@ -41,17 +41,36 @@ struct GemmParams {
   const uint16_t* b;
   uint16_t* y;
   int M, N, K;
-  int tiles_m, tiles_n;
+  int tiles_m, tiles_n;  // 256 x 256 tiles
+  int tile0;             // first tile (in walk order) of this launch
+  int quarter;           // 1: each workgroup computes one 128 x 128 quarter of a tile
+};
+
+template <int BM, int BN>
+struct GemmCfg {
+  static constexpr int WM = BM / 2, WN = BN / 4;  // wave tile (2 x 4 waves)
+  static constexpr int I = WM / 32, J = WN / 32;  // MFMA 32x32 blocks per wave
+  static constexpr int AJ = BM / 64;              // activation chunks per thread per step
+  static constexpr int WPT = BN / 64;             // code words per thread per step
+  static constexpr int TPC = 8 / WPT;             // threads per weight column
+  static constexpr int LDC = BN + 8;              // LDS row pitch (bf16) of the output tile
+  static constexpr size_t kSmem = (size_t)2 * (BM + BN) * LDK * sizeof(uint16_t);
+  static_assert((size_t)BM * LDC * sizeof(uint16_t) <= kSmem, "output tile fits the K-step stages");
+  static_assert(I >= 1 && J >= 1 && (WPT == 2 || WPT == 4) && AJ % 2 == 0, "tile shape");
 };
 
 // One K step's raw inputs held by a thread.
+template <class C>
 struct Raw {
-  u32x4 a[4];      // activations: rows a_r0 + 64 j of the tile, 16-byte chunk a_kc of the step
-  u32x4 w;         // code words 4 * b_half .. 4 * b_half + 3 of column n0 + b_col (half a group)
+  u32x4 a[C::AJ];  // activations: rows a_r0 + 64 j of the tile, 16-byte chunk a_kc of the step
+  u32x4 w;         // code words WPT * b_part .. + WPT - 1 of column n0 + b_col
   uint32_t s, b;   // that group's scale and bias (bf16 bits)
 };
 
+template <int BM, int BN>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
+  using C = GemmCfg<BM, BN>;
+  constexpr int I = C::I, J = C::J, AJ = C::AJ, WPT = C::WPT, LDC = C::LDC;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
   uint16_t* As = smem;                    // [2][BM * LDK]
   uint16_t* Bs = smem + 2 * BM * LDK;     // [2][BN * LDK]
@@ -61,10 +80,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int wave = tid >> 6;
   const int wm = wave >> 2, wn = wave & 3;
 
-  // Tile id: XCD-contiguous remap, then grouped row-major walk.
+  // Tile: XCD-contiguous remap of full-tile launches, then a grouped row-major walk of the
+  // 256 x 256 tiles; a quarter launch gives each tile's four 128 x 128 quarters to four workgroups.
   const int G = gridDim.x;
-  int id = blockIdx.x;
-  if ((G & 7) == 0) id = (id & 7) * (G >> 3) + (id >> 3);
+  int bid = blockIdx.x;
+  int q = 0;
+  if (P.quarter) {
+    q = bid & 3;
+    bid >>= 2;
+  } else if ((G & 7) == 0) {
+    bid = (bid & 7) * (G >> 3) + (bid >> 3);
+  }
+  const int id = P.tile0 + bid;
   const int per_group = kGroupM * P.tiles_n;
   const int group = id / per_group;
   const int first_m = group * kGroupM;
@@ -72,7 +99,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int in_group = id - group * per_group;
   const int tm = first_m + in_group % gm;
   const int tn = in_group / gm;
-  const int m0 = tm * BM, n0 = tn * BN;
+  const int m0 = tm * kTile + (q >> 1) * BM, n0 = tn * kTile + (q & 1) * BN;
   const int nk = P.K / BK;  // even: K % 128 == 0
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
@@ -85,53 +112,58 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
       const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
 
   // Loader roles. Activations: 16-byte chunk a_kc of rows a_r0 + 64 j (row j's offset goes in the
-  // scalar offset). Weights: words 4 * b_half .. + 3 of column n0 + b_col.
+  // scalar offset). Weights: words WPT * b_part .. + WPT - 1 of column n0 + b_col.
   const int a_kc = tid & 7;
   const int a_r0 = tid >> 3;
   const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
   const int xrow64 = 64 * P.K * 2;
-  const int b_col = tid >> 1, b_half = tid & 1;
+  const int b_col = tid / C::TPC, b_part = tid % C::TPC;
   const uint32_t col = (uint32_t)(n0 + b_col);
-  const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)b_half * 16u;
+  const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)(b_part * WPT * 4);
   const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
 
-  Raw raw[2];
+  Raw<C> raw[2];
   // Steps past the last are clamped to it (their data is written to an LDS stage nobody reads).
-  auto load = [&](int kt, Raw& R) {
+  auto load = [&](int kt, Raw<C>& R) {
     const int k = kt < nk ? kt : nk - 1;
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < AJ; ++j)
       R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrow64, 0);
-    R.w = __builtin_amdgcn_raw_buffer_load_b128(rw, woff, k * 32, 0);
+    if constexpr (WPT == 4) {
+      R.w = __builtin_amdgcn_raw_buffer_load_b128(rw, woff, k * 32, 0);
+    } else {
+      const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rw, woff, k * 32, 0);
+      R.w = u32x4{t.x, t.y, 0u, 0u};
+    }
     R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
     R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
   };
-  auto store_a = [&](const Raw& R, int st, int j0, int j1) {
+  auto store_a = [&](const Raw<C>& R, int st, int j0, int j1) {
     uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
 #pragma unroll
     for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + 64 * j * LDK) = R.a[j];
   };
-  auto store_b_fast = [&](const Raw& R, int st, int j0, int j1) {
-    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_half * 32;
+  auto store_b_fast = [&](const Raw<C>& R, int st, int j0, int j1) {
+    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
     const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
     const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
 #pragma unroll
     for (int j = j0; j < j1; ++j)
       *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j], s24, s20, bf);
   };
-  auto store_b_exact = [&](const Raw& R, int st) {
-    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_half * 32;
+  auto store_b_exact = [&](const Raw<C>& R, int st) {
+    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
     const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
 #pragma unroll
-    for (int j = 0; j < 4; ++j)
+    for (int j = 0; j < WPT; ++j)
       *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j], sf, sf * 0.0625f, bf);
   };
 
-  f32x16 acc[4][2];
+  f32x16 acc[I][J];
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < I; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j)
+    for (int j = 0; j < J; ++j)
 #pragma unroll
       for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
 
@@ -142,26 +174,26 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   // other stage; then step kt + 3 is loaded into the registers just written out.
   auto step = [&](int kt, auto parity) {
     constexpr int ST = decltype(parity)::value;
-    Raw& R = raw[ST ^ 1];
-    const uint16_t* as = As + ST * BM * LDK + (wm * 128 + lrow) * LDK + lk;
-    const uint16_t* bs = Bs + ST * BN * LDK + (wn * 64 + lrow) * LDK + lk;
+    Raw<C>& R = raw[ST ^ 1];
+    const uint16_t* as = As + ST * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
+    const uint16_t* bs = Bs + ST * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
 #pragma unroll
     for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 Af[4], Bf[2];
+      bf16x8 Af[I], Bf[J];
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < I; ++i)
         Af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
 #pragma unroll
-      for (int j = 0; j < 2; ++j)
+      for (int j = 0; j < J; ++j)
         Bf[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
 #pragma unroll
-      for (int i = 0; i < 4; ++i)
+      for (int i = 0; i < I; ++i)
 #pragma unroll
-        for (int j = 0; j < 2; ++j) acc[i][j] = Mfma<32>::mma(Af[i], Bf[j], acc[i][j]);
-      if (ks == 0) store_a(R, ST ^ 1, 0, 2);
-      if (ks == 1) store_a(R, ST ^ 1, 2, 4);
-      if (ks == 2) store_b_fast(R, ST ^ 1, 0, 2);
-      if (ks == 3) store_b_fast(R, ST ^ 1, 2, 4);
+        for (int j = 0; j < J; ++j) acc[i][j] = Mfma<32>::mma(Af[i], Bf[j], acc[i][j]);
+      if (ks == 0) store_a(R, ST ^ 1, 0, AJ / 2);
+      if (ks == 1) store_a(R, ST ^ 1, AJ / 2, AJ);
+      if (ks == 2) store_b_fast(R, ST ^ 1, 0, WPT / 2);
+      if (ks == 3) store_b_fast(R, ST ^ 1, WPT / 2, WPT);
     }
     if (!fast_scale_ok(R.s)) store_b_exact(R, ST ^ 1);
     __syncthreads();
@@ -174,8 +206,8 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   // Prologue: steps 0 and 1 in registers, step 0 in LDS, step 2 in flight.
   load(0, raw[0]);
   load(1, raw[1]);
-  store_a(raw[0], 0, 0, 4);
-  store_b_fast(raw[0], 0, 0, 4);
+  store_a(raw[0], 0, 0, AJ);
+  store_b_fast(raw[0], 0, 0, WPT);
   if (!fast_scale_ok(raw[0].s)) store_b_exact(raw[0], 0);
   load(2, raw[0]);
   __syncthreads();
@@ -185,28 +217,28 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
     step(kt + 1, std::integral_constant<int, 1>{});
   }
 
-  // Epilogue: the 256 x 256 tile as bf16 through LDS (every wave is past the last step's reads),
-  // then 16-byte row chunks; rows past M fall outside y's buffer resource, columns past N are skipped
+  // Epilogue: the tile as bf16 through LDS (every wave is past the last step's reads), then
+  // 16-byte row chunks; rows past M fall outside y's buffer resource, columns past N are skipped
   // (N % 16 == 0, so a chunk is entirely inside or outside).
   uint16_t* Cs = smem;
 #pragma unroll
-  for (int i = 0; i < 4; ++i)
+  for (int i = 0; i < I; ++i)
 #pragma unroll
-    for (int j = 0; j < 2; ++j) {
-      const int n = wn * 64 + j * 32 + lrow;
+    for (int j = 0; j < J; ++j) {
+      const int n = wn * C::WN + j * 32 + lrow;
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const int m = wm * 128 + i * 32 + Mfma<32>::row(lane, r);
+        const int m = wm * C::WM + i * 32 + Mfma<32>::row(lane, r);
         Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
       }
     }
   __syncthreads();
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
       P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+  constexpr int kChunksPerRow = BN / 8;
 #pragma unroll 4
-  for (int q = 0; q < BM * BN / 8 / kThreads; ++q) {
-    const int c = tid + q * kThreads;
-    const int r = c >> 5, ch = c & 31;
+  for (int c = tid; c < BM * kChunksPerRow; c += kThreads) {
+    const int r = c / kChunksPerRow, ch = c % kChunksPerRow;
     const int gn = n0 + ch * 8;
     if (gn < P.N) {
       const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
@@ -215,28 +247,50 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   }
 }
 
-constexpr size_t kSmemBytes = (size_t)2 * (BM + BN) * LDK * sizeof(uint16_t);
-static_assert((size_t)BM * LDC * sizeof(uint16_t) <= kSmemBytes, "output tile fits the K-step stages");
-
-}  // namespace
-
-hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                       const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream) {
+template <int BM, int BN>
+hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kSmemBytes);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)GemmCfg<BM, BN>::kSmem);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
+  constexpr size_t smem = GemmCfg<BM, BN>::kSmem;
+  hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3(blocks), dim3(kThreads), smem, stream, P);
+  return hipGetLastError();
+}
+
+}  // namespace
+
+// Whole rounds of 256 x 256 tiles (one per CU at a time) in one launch; when the last round would
+// leave most CUs idle, its tiles are cut into 128 x 128 quarters and launched next, so that round
+// runs on four times as many CUs at about a third of a tile's time.
+hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y,
+                       int M, int N, int K, int cus, hipStream_t stream) {
   GemmParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
-  P.tiles_m = (M + BM - 1) / BM;
-  P.tiles_n = (N + BN - 1) / BN;
-  const unsigned blocks = (unsigned)(P.tiles_m * P.tiles_n);
-  hipLaunchKernelGGL(gemm_kernel, dim3(blocks), dim3(kThreads), kSmemBytes, stream, P);
-  return hipGetLastError();
+  P.tiles_m = (M + kTile - 1) / kTile;
+  P.tiles_n = (N + kTile - 1) / kTile;
+  const int total = P.tiles_m * P.tiles_n;
+  const int c = cus > 0 ? cus : 1;
+  const int rem = total % c;
+  const int tail = (rem > 0 && 4 * rem <= 2 * c) ? rem : 0;
+  const int main_tiles = total - tail;
+  if (main_tiles > 0) {
+    P.tile0 = 0;
+    P.quarter = 0;
+    hipError_t e = launch_tiles<256, 256>(P, main_tiles, stream);
+    if (e != hipSuccess) return e;
+  }
+  if (tail > 0) {
+    P.tile0 = main_tiles;
+    P.quarter = 1;
+    hipError_t e = launch_tiles<128, 128>(P, 4 * tail, stream);
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 }  // namespace qmm4

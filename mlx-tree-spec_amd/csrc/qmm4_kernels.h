@@ -50,7 +50,7 @@ hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 
 // LDS-tiled MFMA GEMM for M > 64.
 hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                       const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream);
+                       const uint16_t* b, uint16_t* y, int M, int N, int K, int cus, hipStream_t stream);
 
 // Bit-exact dequantization to bf16 [N, K].
 hipError_t launch_dequant(const uint32_t* w, const uint16_t* s, const uint16_t* b,
