@@ -256,7 +256,7 @@ def main() -> int:
     traffic = None
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE and
     # WRITE_SIZE passes (scaled by a copy of known size); null when that summary is absent.
-    tpath = os.path.join(ROOT, "profiles", "skinny_decode_gate_up_traffic.txt")
+    tpath = os.path.join(ROOT, "profiles", "rowsplit_decode_gate_up_traffic.txt")
     if os.path.exists(tpath):
         with open(tpath) as f:
             for ln in f:
@@ -273,7 +273,7 @@ def main() -> int:
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qmm4::skinny_kernel<qmm4::SkinnyCfg<4, 4, 1, 2, 4, 12>> (rows <= 4, resident x)",
+                     "kernel": "qmm4::rowsplit_kernel<5> (rows <= 4, one workgroup per CU owning 136 weight rows)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
                      "bytes_per_launch": round(statistics.mean(byts))},
         "workloads": out_workloads,
