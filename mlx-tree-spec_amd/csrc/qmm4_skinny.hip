@@ -54,7 +54,7 @@ struct SkinnyParams {
   long long U;    // units = T * NS
 };
 
-template <int MP_, int V_, int CT_, int PF_, int WPE_, int XS_>
+template <int MP_, int V_, int CT_, int PF_, int WPE_, int XS_, int WAVES_ = 4>
 struct SkinnyCfg {
   static constexpr int MP = MP_;               // rows served (M <= MP), a power of two
   static constexpr int MB = (MP + 15) / 16;    // 16-row MFMA blocks
@@ -62,7 +62,7 @@ struct SkinnyCfg {
   static constexpr int CT = CT_, PF = PF_;
   static_assert(PF >= 1 && PF <= 4, "prefetch depth 1..4");
   static constexpr int kWavesPerSimd = WPE_;  // register budget: 512 / WPE VGPRs+AGPRs per lane
-  static constexpr int kWaves = 4;
+  static constexpr int kWaves = WAVES_;         // waves per workgroup (each owns CT column blocks)
   static constexpr int kThreads = 64 * kWaves;
   static constexpr int CW = kWaves * CT * 16;  // columns per tile
   static constexpr int XU = MP * V * 16;       // 16-byte units of a step's x slice
@@ -555,36 +555,55 @@ void skinny_kernel(SkinnyParams P) {
   }
 }
 
-// Kernel table: id -> (rows, V, CT, PF, waves per SIMD, resident x slots). The x slice of a step
+// Kernel table: id -> (rows, V, CT, PF, waves per SIMD, resident x slots, waves per workgroup).
+// The x slice of a step
 // is at most 16 KB (rows * V <= 64), so larger row counts take shorter steps; V = 2 and 1 also
 // serve K that four super-steps do not divide. Variants 12-14 are the resident-x twins of 0-2
 // (48 KB of x slots each, three workgroups per CU).
 #ifndef QMM4_SKINNY_PF_SMALL
 #define QMM4_SKINNY_PF_SMALL 2  // prefetch depth of the variants for up to 16 rows
 #endif
+#ifndef QMM4_SKINNY_WAVES32
+#define QMM4_SKINNY_WAVES32 12  // 17-32 rows: 192-column tiles, one x staging per 12 waves
+#endif
+#ifndef QMM4_SKINNY_WAVES64
+#define QMM4_SKINNY_WAVES64 4
+#endif
 #ifndef QMM4_SKINNY_PF_RX
 #define QMM4_SKINNY_PF_RX 2     // prefetch depth of the resident-x variants
 #endif
 #define QMM4_SKINNY_VARIANTS(X) \
-  X(0, 4, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0)   \
-  X(1, 8, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0)   \
-  X(2, 16, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0)  \
-  X(3, 32, 2, 1, 2, 4, 0)                     \
-  X(4, 64, 1, 1, 2, 4, 0)                     \
-  X(5, 4, 2, 1, 2, 4, 0)                      \
-  X(6, 8, 2, 1, 2, 4, 0)                      \
-  X(7, 16, 2, 1, 2, 4, 0)                     \
-  X(8, 4, 1, 1, 2, 4, 0)                      \
-  X(9, 8, 1, 1, 2, 4, 0)                      \
-  X(10, 16, 1, 1, 2, 4, 0)                    \
-  X(11, 32, 1, 1, 2, 4, 0)                    \
-  X(12, 4, 4, 1, QMM4_SKINNY_PF_RX, 4, 12)    \
-  X(13, 8, 4, 1, QMM4_SKINNY_PF_RX, 4, 6)     \
-  X(14, 16, 4, 1, QMM4_SKINNY_PF_RX, 4, 3)
+  X(0, 4, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0, 4)   \
+  X(1, 8, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0, 4)   \
+  X(2, 16, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0, 4)  \
+  X(3, 32, 2, 1, 2, 4, 0, QMM4_SKINNY_WAVES32)                     \
+  X(4, 64, 1, 1, 2, 4, 0, QMM4_SKINNY_WAVES64)                     \
+  X(5, 4, 2, 1, 2, 4, 0, 4)                      \
+  X(6, 8, 2, 1, 2, 4, 0, 4)                      \
+  X(7, 16, 2, 1, 2, 4, 0, 4)                     \
+  X(8, 4, 1, 1, 2, 4, 0, 4)                      \
+  X(9, 8, 1, 1, 2, 4, 0, 4)                      \
+  X(10, 16, 1, 1, 2, 4, 0, 4)                    \
+  X(11, 32, 1, 1, 2, 4, 0, 4)                    \
+  X(12, 4, 4, 1, QMM4_SKINNY_PF_RX, 4, 12, 4)    \
+  X(13, 8, 4, 1, QMM4_SKINNY_PF_RX, 4, 6, 4)     \
+  X(14, 16, 4, 1, QMM4_SKINNY_PF_RX, 4, 3, 4)
 
-#define QMM4_CFG_TYPE(id, mp, v, ct, pf, wpe, xs) typedef SkinnyCfg<mp, v, ct, pf, wpe, xs> SkCfg##id;
+#define QMM4_CFG_TYPE(id, mp, v, ct, pf, wpe, xs, wv) typedef SkinnyCfg<mp, v, ct, pf, wpe, xs, wv> SkCfg##id;
 QMM4_SKINNY_VARIANTS(QMM4_CFG_TYPE)
 #undef QMM4_CFG_TYPE
+
+// Columns per tile of a variant: the kernel's CW. The host sizes the split-K partials (and the
+// tile count) from this, so it must be the kernel's own constant.
+static int skinny_tile_cols(int variant) {
+  switch (variant) {
+#define QMM4_CW_OF(id, mp, v, ct, pf, wpe, xs, wv) \
+  case id: return SkCfg##id::CW;
+    QMM4_SKINNY_VARIANTS(QMM4_CW_OF)
+#undef QMM4_CW_OF
+    default: return 0;
+  }
+}
 
 int skinny_variant(int M, int vmax, int* tile_cols, int* steps_v) {
   const int mp = M <= 4 ? 4 : M <= 8 ? 8 : M <= 16 ? 16 : M <= 32 ? 32 : 64;
@@ -595,7 +614,7 @@ int skinny_variant(int M, int vmax, int* tile_cols, int* steps_v) {
   else if (v == 4) id = mp == 4 ? 0 : mp == 8 ? 1 : 2;
   else if (v == 2) id = mp == 4 ? 5 : mp == 8 ? 6 : mp == 16 ? 7 : 3;
   else id = mp == 4 ? 8 : mp == 8 ? 9 : mp == 16 ? 10 : 11;
-  *tile_cols = 64;  // every variant: 4 waves x 1 column block x 16 columns
+  *tile_cols = skinny_tile_cols(id);
   *steps_v = v;
   return id;
 }
@@ -620,9 +639,19 @@ int skinny_resident_twin(int variant, int* slots) {
   }
 }
 
+static int skinny_threads(int variant) {
+  switch (variant) {
+#define QMM4_THREADS(id, mp, v, ct, pf, wpe, xs, wv) \
+  case id: return SkCfg##id::kThreads;
+    QMM4_SKINNY_VARIANTS(QMM4_THREADS)
+#undef QMM4_THREADS
+    default: return 256;
+  }
+}
+
 static const void* skinny_func(int variant) {
   switch (variant) {
-#define QMM4_FUNC(id, mp, v, ct, pf, wpe, xs) \
+#define QMM4_FUNC(id, mp, v, ct, pf, wpe, xs, wv) \
   case id: return reinterpret_cast<const void*>(&skinny_kernel<SkCfg##id>);
     QMM4_SKINNY_VARIANTS(QMM4_FUNC)
 #undef QMM4_FUNC
@@ -633,7 +662,7 @@ static const void* skinny_func(int variant) {
 int skinny_occupancy(int variant) {
   int nb = 0;
   const void* f = skinny_func(variant);
-  if (!f || hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, 256, 0) != hipSuccess) return 1;
+  if (!f || hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, skinny_threads(variant), 0) != hipSuccess) return 1;
   return nb > 0 ? nb : 1;
 }
 
@@ -643,9 +672,9 @@ hipError_t launch_skinny(const SkinnyPlan& plan, const uint16_t* x, const uint32
   SkinnyParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y; P.part = part; P.cnt = cnt;
   P.M = M; P.N = N; P.K = K; P.NS = K / (128 * plan.steps_v); P.G = plan.blocks; P.U = plan.units;
-  const dim3 grid((unsigned)plan.blocks), block(256);
+  const dim3 grid((unsigned)plan.blocks), block((unsigned)skinny_threads(plan.variant));
   switch (plan.variant) {
-#define QMM4_LAUNCH(id, mp, v, ct, pf, wpe, xs) \
+#define QMM4_LAUNCH(id, mp, v, ct, pf, wpe, xs, wv) \
   case id: hipLaunchKernelGGL(skinny_kernel<SkCfg##id>, grid, block, 0, stream, P); break;
     QMM4_SKINNY_VARIANTS(QMM4_LAUNCH)
 #undef QMM4_LAUNCH
