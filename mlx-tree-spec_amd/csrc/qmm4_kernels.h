@@ -36,7 +36,7 @@ struct RowSplitPlan {
   int V;        // super-steps (128 k) per unit
   int R;        // weight rows per workgroup
   int RB;       // 16-row blocks per workgroup
-  int IPW;      // super-steps per wave range
+  int SU;       // units per block (K / (128 V))
   int blocks;   // workgroups
   size_t smem;  // dynamic LDS bytes
 };

@@ -3,24 +3,31 @@
 // Same arithmetic and operand layout as the skinny kernel (qmm4_skinny.hip; replaces the
 // reference's qmv_packed and 8/16-row NAX kernels for decode, src/mlx_tree_spec/qmm_packed.py:
 // 151-220, 428-557), with a decomposition for the case where the output columns alone fill the
-// GPU: workgroup p (one per CU, 12 waves) owns the R consecutive weight rows [p R, p R + R) over
+// GPU: workgroup p (one per CU, 16 waves) owns the R consecutive weight rows [p R, p R + R) over
 // the whole of K, so workgroups share nothing and no partial sums leave a CU.
 //
-//  * Inside a workgroup, the RB = ceil(R / 16) row blocks x K/128 super-steps are one sequence
-//    (block-major) cut into 12 equal contiguous wave ranges; a wave streams its range as one
-//    pipeline of units of V super-steps (weights PF units ahead in a register ring), and
-//    accumulates each block it touches with MFMA 16x16x32 (bf16, fp32 accumulation).
-//  * Loads: lane (n = lane % 16, g = lane / 16) of a wave holds weight row 16 b + n of its block;
-//    in a unit it loads V 16-byte pieces of that row, piece v at byte 64 v + 16 g of the unit's
-//    V * 64-byte run, so each row is read as one contiguous run per unit. Rows past the workgroup's
-//    range read as zero (an offset outside the buffer resource), as do prefetches past a wave's
-//    range (a zero-length resource).
-//  * x (M <= 4 rows, whole K) is staged once in LDS in A-fragment order, behind the first weight
-//    prefetches; the stream has no barrier.
+//  * Work units: the RB = ceil(R / 16) row blocks x SU = K / (128 V) steps of V super-steps (128 k)
+//    each; unit u = b * SU + st. Waves take units from a counter in LDS as they free up, with
+//    PF = 2 units in flight per wave (a register ring), so a wave the SIMD arbiter favours simply
+//    does more units and every wave of a SIMD keeps working until the units run out. (A fixed split
+//    leaves the youngest wave of each SIMD running alone for the last fifth of the stream.) A
+//    wave's issue priority also falls with the units it has done, so that the oldest wave does
+//    not take the units while the youngest sits on the two in its ring. V = 4 where K allows
+//    (a unit then covers whole 128-byte lines of each row), else 5.
+//  * Loads: lane (n = lane % 16, g = lane / 16) holds weight row 16 b + n of the unit's block; it
+//    loads V 16-byte pieces of that row, piece v at byte 64 v + 16 g of the unit's V * 64-byte run,
+//    so each row is read as one contiguous run per unit. Rows past the workgroup's range read as
+//    zero (an offset outside the buffer resource), as do fetches past the last unit (a zero-length
+//    resource).
+//  * x (M <= 4 rows, whole K) is staged once in LDS in A-fragment order. Every wave issues its x
+//    loads before any wave issues a weight fetch (a bare barrier between the two), and the stores
+//    wait for the x loads alone (the vector memory counter is in order).
 //  * Dequantization: dequant_word_fast, or dequant_word for a unit in which one of the wave's
 //    rows has a scale outside the fast form's range (a wave-uniform branch per unit).
-//  * At the end each wave leaves its per-block fp32 sums in LDS; after one barrier the workgroup
-//    adds the contributions to each block in wave order (deterministic) and writes bf16 y.
+//  * Each unit's fp32 sums (MFMA 16x16x32, bf16 inputs) go to their own LDS slot: only lanes
+//    g = 0 hold x rows 0..3, so a slot is 16 lanes x 16 bytes. After one barrier the workgroup adds
+//    the slots of each block in step order (deterministic whatever wave ran which unit) and
+//    writes bf16 y.
 #include <type_traits>
 
 #include "qmm4_common.h"
@@ -30,12 +37,11 @@ namespace qmm4 {
 
 namespace {
 
-constexpr int kRsWaves = 12;
+constexpr int kRsWaves = 16;
 constexpr int kRsThreads = 64 * kRsWaves;
 constexpr int kRsMP = 4;  // x rows held per fragment (M <= 4)
-constexpr int kRsPF = 2;
-// A wave's range covers at most two row blocks (the launch keeps a range no longer than K).
-constexpr int kRsSlots = 2;
+constexpr int kRsPF = 2;  // units in flight per wave
+constexpr int kRsXB = 4;  // x pieces per thread per staging batch
 
 struct RowSplitParams {
   const uint16_t* x;
@@ -44,9 +50,9 @@ struct RowSplitParams {
   const uint16_t* b;
   uint16_t* y;
   int M, N, K;
-  int R;    // weight rows per workgroup (a multiple of 8)
-  int RB;   // 16-row blocks per workgroup, ceil(R / 16)
-  int IPW;  // super-steps (128 k) per wave range, a multiple of V, at most K / 128
+  int R;   // weight rows per workgroup (a multiple of 8)
+  int RB;  // 16-row blocks per workgroup, ceil(R / 16)
+  int SU;  // units per block, K / (128 V)
 };
 
 template <int V>
@@ -69,30 +75,72 @@ __device__ __forceinline__ Scales<V> load_scales(__amdgpu_buffer_rsrc_t r, uint3
   return o;
 }
 
+// Dynamic LDS: x pieces [S][16][kRsMP] (A-fragment order), unit slots [U][16] f32x4, a spare
+// 16-byte slot (the target of surplus x pieces, so that every x store is unconditional), the counter.
+__host__ __device__ inline size_t rowsplit_xs_bytes(int K) { return (size_t)(K >> 7) * 16 * kRsMP * 16; }
+__host__ __device__ inline size_t rowsplit_part_bytes(int units) { return (size_t)units * 16 * 16; }
+
 template <int V>
-__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(3)))
+__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int S = P.K >> 7;                       // super-steps per row
-  const int SU = S / V;                         // units per row block
-  u32x4* xs = reinterpret_cast<u32x4*>(lds);    // [S][16][kRsMP] x pieces (A-fragment order)
-  f32x4* part = reinterpret_cast<f32x4*>(lds + (size_t)S * 16 * kRsMP * sizeof(u32x4));  // [waves][slots][64]
+  const int S = P.K >> 7;  // super-steps per row
+  const int SU = P.SU;
+  const int U = P.RB * SU;
+  u32x4* xs = reinterpret_cast<u32x4*>(lds);
+  f32x4* part = reinterpret_cast<f32x4*>(lds + rowsplit_xs_bytes(P.K));
+  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.K) + rowsplit_part_bytes(U));
+  int* next = reinterpret_cast<int*>(spare + 1);
 
   const int tid = threadIdx.x;
-  // The wave index is uniform across the wave; readfirstlane tells the compiler so (the wave's
-  // range then lives in scalar registers and its buffer resources need no per-lane loop).
+  // The wave index is uniform across the wave; readfirstlane tells the compiler so (unit indices
+  // then live in scalar registers and buffer resources need no per-lane loop).
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * P.R;
   const int r1 = min(P.N, r0 + P.R);
   const int KG = P.K >> 6;
 
-  // This wave's range, in units of the workgroup's block-major sequence.
-  const int su0 = wave * P.IPW;
-  const int su1 = min(su0 + P.IPW, P.RB * S);
-  const int ub = su0 / V, ue = su1 > su0 ? su1 / V : ub;
-  const int nunits = ue - ub;
-  const int b_first = su0 / S;
+  // x pieces: item i = sq * M + m is the 16-byte piece sq (k = 8 sq .. 8 sq + 7) of row m, stored
+  // at LDS position sq * kRsMP + m. All batches but the last are staged before any weight fetch;
+  // the last batch is loaded before the first fetches and stored after them. Loads past the last
+  // item go to an offset outside the buffer resource (zeros, no memory access); the stores are
+  // unconditional (surplus pieces go to the spare slot): a store under a branch would let the
+  // compiler move its load there, behind the fetches, and wait for all of them.
+  const int xitems = S * 16 * P.M;
+  const int nxb = (xitems + kRsThreads * kRsXB - 1) / (kRsThreads * kRsXB);
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
+  u32x4 xr[kRsXB];
+  auto load_x = [&](int batch) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kRsXB; ++j) {
+      const int i = tid + (batch * kRsXB + j) * kRsThreads;
+      const int sq = i / P.M, m = i - sq * P.M;
+      const uint32_t off = i < xitems ? ((uint32_t)m * (uint32_t)P.K + (uint32_t)sq * 8u) * 2u : 0x80000000u;
+      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    }
+  };
+  auto store_x = [&](int batch) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < kRsXB; ++j) {
+      const int i = tid + (batch * kRsXB + j) * kRsThreads;
+      const int sq = i / P.M, m = i - sq * P.M;
+      u32x4* dst = i < xitems ? xs + (sq * kRsMP + m) : spare;
+      *dst = xr[j];
+    }
+  };
+  for (int bt = 0; bt + 1 < nxb; ++bt) {
+    load_x(bt);
+    store_x(bt);
+  }
+  load_x(nxb - 1);
+  // Every wave's x loads enter the CU's memory pipeline before any weight fetch: the pipeline
+  // returns data in order, so an x load queued behind other waves' fetches would wait for them.
+  // (A bare s_barrier: no fence, so no wait for the loads themselves.)
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
 
   const int wrec = rsrc_bytes((unsigned long long)P.N * (P.K >> 1));
   const int srec = rsrc_bytes((unsigned long long)P.N * KG * 2);
@@ -102,11 +150,10 @@ void rowsplit_kernel(RowSplitParams P) {
 
   u32x4 wv[kRsPF][V];
   Scales<V> sv[kRsPF], bv[kRsPF];
-  int fi = 0;        // index of the next unit to fetch, relative to ub
-  auto fetch = [&](int j) __attribute__((always_inline)) {
-    const bool live = fi < nunits;
-    const int u = ub + (live ? fi : 0);
-    const int b = u / SU, st = u - b * SU;
+  auto fetch = [&](int j, int u) __attribute__((always_inline)) {
+    const bool live = u < U;
+    const int uu = live ? u : 0;
+    const int b = uu / SU, st = uu - b * SU;
     const int row = r0 + b * 16 + n;
     const uint32_t wo = row < r1 ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
     const uint32_t so = row < r1 ? (uint32_t)row * (uint32_t)KG * 2u : kOut;
@@ -120,30 +167,25 @@ void rowsplit_kernel(RowSplitParams P) {
     for (int v = 0; v < V; ++v) wv[j][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + v * 64, st * V * 64, 0);
     sv[j] = load_scales<V>(rs, so, st * 4 * V);
     bv[j] = load_scales<V>(rb, so, st * 4 * V);
-    ++fi;
   };
-#pragma unroll
-  for (int j = 0; j < kRsPF; ++j) fetch(j);
+  // The ring holds units in the order they were taken, so the first unit past the end ends it.
+  int ua = wave, ub = wave + kRsWaves;
+  fetch(0, ua);
+  fetch(1, ub);
+  __builtin_amdgcn_sched_barrier(0);
 
-  // x, whole K, behind the first prefetches: piece (ss, q) of row m at ((ss * 16 + q) * MP + m).
-  for (int i = tid; i < S * 16 * kRsMP; i += kRsThreads) {
-    const int m = i & (kRsMP - 1), sq = i >> 2;
-    if (m < P.M) xs[sq * kRsMP + m] = *reinterpret_cast<const u32x4*>(P.x + (size_t)m * P.K + (size_t)sq * 8);
-  }
+  store_x(nxb - 1);
+  if (tid == 0) *next = kRsPF * kRsWaves;
   __syncthreads();
 
   const int aoff = g * 4 * kRsMP + min(n, P.M - 1);
-  f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
-  int b_cur = b_first;
-
-  auto flush = [&](int b) __attribute__((always_inline)) {
-    part[(wave * kRsSlots + (b - b_first)) * 64 + lane] = acc;
-    acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  };
+  int ndone = 0;
+  __builtin_amdgcn_s_setprio(3);
 
   auto compute = [&](int j, int st, auto fast) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast)::value;
     const u32x4* xb = xs + (size_t)st * V * 16 * kRsMP;
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int e2 = 2 * v + (g >> 1);
@@ -159,68 +201,67 @@ void rowsplit_kernel(RowSplitParams P) {
                                                       0, 0, 0);
       }
     }
+    return acc;
   };
 
-  // One unit: consume ring slot J, refill it, close the block when it ends here.
-  auto unit = [&](int i, auto jc) __attribute__((always_inline)) {
+  // One unit from ring slot J: take the next unit index (its LDS round trip overlaps the MFMAs),
+  // compute, leave the sums in the unit's slot, refill the slot.
+  auto unit = [&](int& u, auto jc) __attribute__((always_inline)) {
     constexpr int j = decltype(jc)::value;
-    const int u = ub + i;
+    int taken = 0;
+    if (lane == 0) taken = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+    const int nu = __builtin_amdgcn_readfirstlane(taken);
     const int b = u / SU, st = u - b * SU;
-    if (b != b_cur) {
-      flush(b_cur);
-      b_cur = b;
-    }
     bool bad = false;
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int e2 = 2 * v + (g >> 1);
       bad |= !fast_scale_ok((sv[j].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
     }
+    f32x4 acc;
     if (__builtin_amdgcn_ballot_w64(bad) == 0)
-      compute(j, st, std::true_type{});
+      acc = compute(j, st, std::true_type{});
     else
-      compute(j, st, std::false_type{});
-    fetch(j);
+      acc = compute(j, st, std::false_type{});
+    if (g == 0) part[u * 16 + n] = acc;
+    ++ndone;
+    // A wave's issue priority falls with the units it has done: the SIMD arbiter otherwise
+    // favours the oldest wave, which then takes most units while the youngest holds its ring's
+    // two units to the end and finishes them alone.
+    if (ndone == 1) __builtin_amdgcn_s_setprio(2);
+    else if (ndone == 2) __builtin_amdgcn_s_setprio(1);
+    else if (ndone == 3) __builtin_amdgcn_s_setprio(0);
+    u = nu;
+    fetch(j, u);
   };
 
-  int i = 0;
-  for (; i + kRsPF <= nunits; i += kRsPF) {
-    unit(i, std::integral_constant<int, 0>{});
-    unit(i + 1, std::integral_constant<int, 1>{});
+  for (;;) {
+    if (ua >= U) break;
+    unit(ua, std::integral_constant<int, 0>{});
+    if (ub >= U) break;
+    unit(ub, std::integral_constant<int, 1>{});
   }
-  if (i < nunits) unit(i, std::integral_constant<int, 0>{});
-  if (nunits > 0) flush(b_cur);
   __syncthreads();
 
-  // Sum each block's contributions in wave order; lane (n, g) element r is x row 4 g + r, weight
-  // row 16 b + n of the block.
+  // y[m, row] = sum over the block's steps, in step order, of its unit slots; lane element m of a
+  // slot is x row m.
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
       P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
-  for (int idx = tid; idx < P.RB * 64; idx += kRsThreads) {
-    const int b = idx >> 6, l = idx & 63;
-    const int ln = l & 15, lg = l >> 4;
-    const int row = r0 + b * 16 + ln;
-    if (4 * lg >= P.M || row >= r1) continue;
-    const int w0 = (b * S) / P.IPW, w1 = min(kRsWaves - 1, ((b + 1) * S - 1) / P.IPW);
+  for (int idx = tid; idx < P.RB * 16; idx += kRsThreads) {
+    const int b = idx >> 4, nn = idx & 15;
+    const int row = r0 + b * 16 + nn;
+    if (row >= r1) continue;
     f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int wv2 = w0; wv2 <= w1; ++wv2) {
-      const int slot = b - (wv2 * P.IPW) / S;
-      const f32x4 c = part[(wv2 * kRsSlots + slot) * 64 + l];
+    for (int st = 0; st < SU; ++st) {
+      const f32x4 c = part[(b * SU + st) * 16 + nn];
       sum[0] += c[0]; sum[1] += c[1]; sum[2] += c[2]; sum[3] += c[3];
     }
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int m = 4 * lg + r;
+    for (int m = 0; m < kRsMP; ++m)
       if (m < P.M)
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16x2(sum[r], 0.0f) & 0xFFFFu), ry,
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16x2(sum[m], 0.0f) & 0xFFFFu), ry,
                                               (uint32_t)(m * P.N + row) * 2u, 0, 0);
-    }
   }
-}
-
-template <int V>
-size_t rowsplit_smem(int K) {
-  return (size_t)(K >> 7) * 16 * kRsMP * sizeof(u32x4) + (size_t)kRsWaves * kRsSlots * 64 * sizeof(f32x4);
 }
 
 }  // namespace
@@ -228,22 +269,23 @@ size_t rowsplit_smem(int K) {
 bool rowsplit_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
   if (M < 1 || M > kRsMP || cus < 1) return false;
   const int S = K >> 7;
-  const int V = S % 5 == 0 ? 5 : S % 4 == 0 ? 4 : 0;
+  // Units of 4 super-steps (256 bytes of a row: two whole 128-byte lines) where K allows: a unit
+  // boundary inside a line splits it between two waves' fetches.
+  const int V = S % 4 == 0 ? 4 : S % 5 == 0 ? 5 : 0;
   if (V == 0) return false;
   const int R = ((N + cus - 1) / cus + 7) / 8 * 8;
   const int RB = (R + 15) / 16;
-  // Enough blocks for every wave (a range no longer than one row of K), and the same smem budget.
-  int IPW = (RB * S + kRsWaves - 1) / kRsWaves;
-  IPW = (IPW + V - 1) / V * V;
-  if (RB < 4 || IPW > S) return false;
-  const size_t smem = V == 5 ? rowsplit_smem<5>(K) : rowsplit_smem<4>(K);
+  const int SU = S / V;
+  // At least 4 blocks per workgroup (the decomposition only pays when rows alone fill the GPU).
+  if (RB < 4) return false;
+  const size_t smem = rowsplit_xs_bytes(K) + rowsplit_part_bytes(RB * SU) + 32;
   if (smem > 160 * 1024) return false;
   // Row offsets of this kernel stay below 1 GiB.
   if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 30)) return false;
   plan->V = V;
   plan->R = R;
   plan->RB = RB;
-  plan->IPW = IPW;
+  plan->SU = SU;
   plan->blocks = (N + R - 1) / R;
   plan->smem = smem;
   return true;
@@ -254,7 +296,7 @@ hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const ui
   RowSplitParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
-  P.R = plan.R; P.RB = plan.RB; P.IPW = plan.IPW;
+  P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
   const void* f = plan.V == 5 ? reinterpret_cast<const void*>(&rowsplit_kernel<5>)
                               : reinterpret_cast<const void*>(&rowsplit_kernel<4>);
   static bool attr_set[2] = {false, false};
