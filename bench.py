@@ -273,7 +273,7 @@ def main() -> int:
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qmm4::rowsplit_kernel<5> (rows <= 4, one workgroup per CU owning 136 weight rows)",
+                     "kernel": "qmm4::rowsplit_kernel<4> (rows <= 4, one workgroup per CU owning 136 weight rows)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
                      "bytes_per_launch": round(statistics.mean(byts))},
         "workloads": out_workloads,
