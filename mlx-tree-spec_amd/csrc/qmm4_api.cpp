@@ -43,6 +43,7 @@ bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) %
 struct DeviceInfo {
   int cus = 0;
   int occ[qmm4::kSkinnyVariants] = {};  // resident skinny workgroups per CU, per variant
+  int vocc[qmm4::kVerifyVariants] = {};  // resident verify workgroups per CU, per variant
 };
 
 // Split-K workspace for one (device, stream): [counters | partials]. Counters are zeroed when the
@@ -64,6 +65,7 @@ int device_info(int dev, DeviceInfo** out) {
     hipError_t e = hipDeviceGetAttribute(&d.cus, hipDeviceAttributeMultiprocessorCount, dev);
     if (e != hipSuccess) return hip_fail(e, "hipDeviceGetAttribute(MultiprocessorCount)");
     for (int v = 0; v < qmm4::kSkinnyVariants; ++v) d.occ[v] = qmm4::skinny_occupancy(v);
+    for (int v = 0; v < qmm4::kVerifyVariants; ++v) d.vocc[v] = qmm4::verify_occupancy(v);
     it = g_dev.emplace(dev, d).first;
   }
   *out = &it->second;
@@ -189,6 +191,47 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   int vmax = 4;
   const long long ks = K / 128;
   while (vmax > 1 && (ks % vmax != 0 || !aligned(scales, 4 * vmax) || !aligned(biases, 4 * vmax))) vmax >>= 1;
+#ifndef QMM4_ROWPHASE_MIN_M
+#define QMM4_ROWPHASE_MIN_M 5
+#endif
+#ifndef QMM4_NO_ROWPHASE
+  // The row-phase kernel stages scale rows with 16-byte loads. It serves more than 16 rows, and
+  // up to 16 rows when N gives every wave its own blocks; fewer rows over a small N go to the
+  // verify kernel (its stream-K ranges balance better when there is little work per CU).
+  if (M >= QMM4_ROWPHASE_MIN_M && aligned(scales, 16) && aligned(biases, 16) && K % 512 == 0) {
+    qmm4::RowPhasePlan pplan;
+    if (qmm4::rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) && (M > 16 || pplan.wide)) {
+      uint32_t* pcnt = nullptr;
+      float* ppart = nullptr;
+      if (pplan.S > 1) {
+        rc = get_workspace(dev, stream, (size_t)pplan.ranges * sizeof(uint32_t), pplan.part_bytes, &pcnt, &ppart);
+        if (rc) return rc;
+      }
+      e = qmm4::launch_rowphase(pplan, xb, w, sb, bb, yb, ppart, pcnt, (int)M, (int)N, (int)K, stream);
+      if (e != hipSuccess) return hip_fail(e, "row-phase kernel launch");
+      return QMM4_OK;
+    }
+  }
+#endif
+#ifndef QMM4_VERIFY_MIN_M
+#define QMM4_VERIFY_MIN_M 5
+#endif
+#ifndef QMM4_NO_VERIFY
+  if (M >= QMM4_VERIFY_MIN_M) {
+    qmm4::VerifyPlan vplan;
+    const int vv = qmm4::verify_variant((int)M, vmax);
+    if (qmm4::verify_plan((int)M, (int)N, (int)K, vmax, di->cus, di->vocc[vv], &vplan)) {
+      uint32_t* vcnt = nullptr;
+      float* vpart = nullptr;
+      rc = get_workspace(dev, stream, (size_t)vplan.tiles * sizeof(uint32_t),
+                         vplan.part_bytes, &vcnt, &vpart);
+      if (rc) return rc;
+      e = qmm4::launch_verify(vplan, xb, w, sb, bb, yb, vpart, vcnt, (int)M, (int)N, (int)K, stream);
+      if (e != hipSuccess) return hip_fail(e, "verify kernel launch");
+      return QMM4_OK;
+    }
+  }
+#endif
   qmm4::SkinnyPlan plan;
   plan.variant = qmm4::skinny_variant((int)M, vmax, &plan.tile_cols, &plan.steps_v);
   plan.tiles = (int)((N + plan.tile_cols - 1) / plan.tile_cols);

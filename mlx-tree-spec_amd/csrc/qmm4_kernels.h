@@ -31,6 +31,50 @@ hipError_t launch_skinny(const SkinnyPlan& plan, const uint16_t* x, const uint32
                          const uint16_t* s, const uint16_t* b, uint16_t* y, float* part,
                          uint32_t* cnt, int M, int N, int K, hipStream_t stream);
 
+// Verify-shape kernel (M <= 64): tiles of output columns shared by the waves of a workgroup, which
+// split each tile's k-steps round-robin; stream-K ranges over (tile, step) units.
+struct VerifyPlan {
+  int variant;      // index into the kernel table (see qmm4_verify.hip)
+  int tile_cols;    // output columns per tile (CW)
+  int steps_v;      // super-steps (128 k) per unit (V)
+  int blocks;       // workgroups launched (G)
+  int tiles;        // tiles along N (T)
+  long long units;  // T * K / (128 * V)
+  int threads;      // threads per workgroup
+  size_t lds;       // dynamic LDS bytes
+  size_t part_bytes;  // split-K partial workspace bytes
+};
+constexpr int kVerifyVariants = 10;
+// Variant for M rows when a unit may span up to `vmax` super-steps.
+int verify_variant(int M, int vmax);
+// Resident workgroups per CU for a variant (HIP occupancy API).
+int verify_occupancy(int variant);
+// Fills `plan` for M rows on `cus` CUs with `occ` resident workgroups per CU; false if unsupported.
+bool verify_plan(int M, int N, int K, int vmax, int cus, int occ, VerifyPlan* plan);
+// `part` holds plan.part_bytes, `cnt` tiles zeroed uint32s.
+hipError_t launch_verify(const VerifyPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                         const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
+                         hipStream_t stream);
+
+// Row-phase kernel (M <= 64): each workgroup owns a range of 16-row weight blocks and a range of
+// K phases; x and the scales are staged per phase in LDS; K is split when N is small.
+struct RowPhasePlan {
+  int variant;        // index into the kernel table (see qmm4_rowphase.hip)
+  int BW;             // blocks per range
+  int S;              // workgroups per range (K split)
+  int NP;             // phases along K
+  int ranges;         // block ranges
+  int blocks;         // workgroups = ranges * S
+  size_t lds;         // dynamic LDS bytes
+  size_t part_bytes;  // partial-tile workspace (S > 1)
+  bool wide;          // every workgroup takes all of K (N fills the GPU)
+};
+bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan);
+// `part` holds plan.part_bytes, `cnt` plan.ranges zeroed uint32s (used when plan.S > 1).
+hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                           const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
+                           hipStream_t stream);
+
 // Row-split decode kernel (up to 4 rows, output columns split evenly over one workgroup per CU).
 struct RowSplitPlan {
   int V;        // super-steps (128 k) per unit

@@ -1,0 +1,504 @@
+// Row-phase quantized matmul for M = 1..64 rows: y = x @ dequant(w)^T.
+//
+// Serves the verify shapes (the reference's NAX verify tiles and multi-row kernel,
+// src/mlx_tree_spec/qmm_packed.py:151-220, 296-394) from MLX's own [N, K/8] layout. The design
+// follows from what bounds these shapes on gfx950: the vector memory address unit takes about one
+// lane per clock, so every load instruction costs the same whether it carries 1 KB or 64 useful
+// bytes. Every global load here moves 16 distinct bytes per lane, and x and the scales are read
+// from global memory once per workgroup and phase, not once per wave and step:
+//
+//  * Workgroup p (8 waves, two per SIMD) owns a range of 16-row weight blocks and a range of
+//    phases (PH = 128 V values of k each); the phase ranges of one block range partition K. When
+//    N alone fills the GPU every workgroup takes all of K; otherwise K is split and the
+//    workgroups of a block range add their fp32 partial tiles (the last to finish adds them in
+//    workgroup order, so results are deterministic).
+//  * Wave w owns blocks w, w + 8, w + 16, ... of the range (at most BPW) and holds one whole phase
+//    of their weights in registers while the next phase's weights are in flight (double buffer).
+//    Lane (n = lane % 16, g = lane / 16) loads V 16-byte pieces of row n of each block, piece v at
+//    byte 64 v + 16 g of the row's PH / 2-byte run, so each row is read as one contiguous run.
+//  * Word t of piece v holds k = PH p + 128 v + 32 g + 8 t: the B operand of MFMA 16x16x32 (v, t)
+//    after exact dequantization in registers (dequant_word_fast, bit-identical to
+//    bf16_rne(fp32(s) * q + fp32(b)); a phase holding a scale outside its range takes
+//    dequant_word). The A operand, lane (m, g), is x[m] at the same 8 k; it is read from LDS once
+//    per (v, t) and feeds the MFMAs of all of the wave's blocks.
+//  * The next phase's x slice (A-fragment order) and the scales and biases of the range's rows are
+//    staged in LDS (double-buffered) by the whole workgroup, behind the weight prefetch; one
+//    barrier per phase publishes them.
+//  * The result leaves through LDS as 16-byte row chunks of y (or as fp32 partial tiles).
+#include <type_traits>
+
+#include "qmm4_common.h"
+#include "qmm4_kernels.h"
+
+namespace qmm4 {
+
+namespace {
+
+
+struct RowPhaseParams {
+  const uint16_t* x;
+  const uint16_t* s;
+  const uint16_t* b;
+  const uint32_t* w;
+  uint16_t* y;
+  float* part;    // [G][items] f32x4 partial tiles (K split only)
+  uint32_t* cnt;  // [ranges] arrival counters; zero before and after every launch
+  int M, N, K;
+  int NB;         // 16-row blocks of w (N / 16)
+  int BW;         // blocks per range
+  int S;          // workgroups per range (K split)
+  int NP;         // phases along K
+};
+
+template <int MB_, int V_, int BPW_, int W_>
+struct RpCfg {
+  static constexpr int kRpWaves = W_;  // waves per workgroup
+  static constexpr int kRpThreads = 64 * W_;
+  static constexpr int MB = MB_;      // 16-row blocks of x (M <= 16 MB)
+  static constexpr int MP = 16 * MB;
+  static constexpr int V = V_;        // super-steps (128 k) per phase
+  static constexpr int PH = 128 * V;  // k per phase
+  static constexpr int BPW = BPW_;    // blocks per wave (at most)
+  static constexpr int RW = 16 * kRpWaves * BPW;  // rows per range (at most)
+  static constexpr int kXPieces = V * 16 * MP;    // 16-byte x pieces per phase
+  static constexpr int kSB = 4 * V;               // bytes of scales (or biases) per row and phase
+  static constexpr int WP = 64 / kSB;             // phases per scale window (64 bytes of each row)
+  static constexpr int kWB = WP * kSB;            // window bytes per row and array
+  static constexpr size_t kXBytes = (size_t)kXPieces * 16;
+  static constexpr size_t kWinBytes = (size_t)RW * kWB;  // one array's window
+  static constexpr int kStages = 3;  // x stages: phase p in use, p + 1 staged, p + 2 being staged
+  static constexpr size_t kYBytes = (size_t)MP * RW * 2;   // epilogue: bf16 tile of y
+  static constexpr size_t kMain = kStages * kXBytes + 2 * kWinBytes;
+  static constexpr size_t kLds = (kMain > kYBytes ? kMain : kYBytes);
+  static constexpr int kItems = kRpWaves * BPW * MB * 64;  // f32x4 items of a partial tile
+  static constexpr int kXL = (kXPieces + kRpThreads - 1) / kRpThreads;         // x loads per thread and phase
+  static constexpr int kWL = (RW * (kWB / 16) + kRpThreads - 1) / kRpThreads;  // window loads per thread and array
+  static_assert(V == 2 || V == 4, "phases of 2 or 4 super-steps");
+};
+
+// Device-coherent 16-byte stores and loads (cache policy sc1: coherent across the XCDs' L2s).
+constexpr int kCoherent = 16;
+
+template <class C>
+__global__ __launch_bounds__(C::kRpThreads) __attribute__((amdgpu_waves_per_eu(C::kRpWaves / 4)))
+void rowphase_kernel(RowPhaseParams P) {
+  constexpr int MB = C::MB, MP = C::MP, V = C::V, BPW = C::BPW, RW = C::RW;
+  constexpr int kRpWaves = C::kRpWaves, kRpThreads = C::kRpThreads;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  __shared__ int s_last;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int p = blockIdx.x;
+  const int range = p / P.S, split = p - range * P.S;
+  const int b0 = range * P.BW;
+  const int nbr = min(P.BW, P.NB - b0);  // blocks in this range
+  const int pa = (int)((long long)split * P.NP / P.S);
+  const int pb = (int)((long long)(split + 1) * P.NP / P.S);
+  const int np = pb - pa;
+  const int r0 = b0 * 16;                // first weight row of the range
+  const int nrows = nbr * 16;
+  // This wave's blocks: wave + W j for j < nbw.
+  const int nbw = nbr > wave ? (nbr - wave + kRpWaves - 1) / kRpWaves : 0;
+  const int KG = P.K >> 6;
+
+  const int wrec = rsrc_bytes((unsigned long long)P.N * (P.K >> 1));
+  const int srec = rsrc_bytes((unsigned long long)P.N * KG * 2);
+  const int xrec = rsrc_bytes((unsigned long long)P.M * P.K * 2);
+  // Offset past the end of every buffer (they stay below 2 GiB for this kernel): loads read zero.
+  constexpr uint32_t kOut = 0x80000000u;
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.x), 0, xrec,
+                                                                      kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.s), 0, srec,
+                                                                      kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.b), 0, srec,
+                                                                      kBufferRsrcWord3);
+
+  auto xs = [&](int j) { return reinterpret_cast<u32x4*>(lds + (size_t)j * C::kXBytes); };
+  uint8_t* const ws_s = lds + C::kStages * C::kXBytes;  // scale window [RW][kWB]
+  uint8_t* const ws_b = ws_s + C::kWinBytes;            // bias window
+
+  // ---- staging of one phase's x pieces ----
+  // x piece i = (v * 16 + g4 * 4 + t) * MP + m holds x[m][PH ph + 128 v + 32 g4 + 8 t .. + 8):
+  // the A fragment of MFMA (v, t) for lane (m, g4). Rows m >= M read as zero.
+  u32x4 xr[C::kXL];
+  auto stage_load = [&](int ph, bool live) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < C::kXL; ++j) {
+      const int i = tid + j * kRpThreads;
+      const int m = i % MP, q = i / MP;  // q = v * 16 + g4 * 4 + t
+      const int v = q >> 4, g4 = (q >> 2) & 3, t = q & 3;
+      const uint32_t off = (live && i < C::kXPieces && m < P.M)
+                               ? ((uint32_t)m * (uint32_t)P.K + (uint32_t)(ph * C::PH + 128 * v + 32 * g4 + 8 * t)) * 2u
+                               : kOut;
+      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+    }
+  };
+  auto stage_store = [&](int J) __attribute__((always_inline)) {
+    u32x4* xd = xs(J);
+#pragma unroll
+    for (int j = 0; j < C::kXL; ++j) {
+      const int i = tid + j * kRpThreads;
+      if (i < C::kXPieces) xd[i] = xr[j];
+    }
+  };
+
+  // ---- scale window: groups of phases [ph0, ph0 + WP) of the range's rows, 16-byte pieces of
+  // each row's contiguous run (every scale line is read once per window, not once per phase).
+  // Returns whether this thread saw a scale outside the fast dequantization's range. Blocking:
+  // the caller has made sure that no wave still reads the previous window. ----
+  auto stage_window = [&](int ph0) __attribute__((always_inline)) {
+    constexpr int kPR = C::kWB / 16;  // pieces per row
+    const int g0 = ph0 * (2 * V);     // first group of the window
+    bool bad = false;
+    // Scales, then biases (one array's pieces in registers at a time).
+#pragma unroll
+    for (int arr = 0; arr < 2; ++arr) {
+      u32x4 r[C::kWL];
+#pragma unroll
+      for (int j = 0; j < C::kWL; ++j) {
+        const int i = tid + j * kRpThreads;
+        const int row = i / kPR, pc = i - row * kPR;
+        const bool ok = row < nrows && g0 + pc * 8 < KG;
+        const uint32_t off = ok ? (uint32_t)(r0 + row) * (uint32_t)KG * 2u + (uint32_t)(g0 + pc * 8) * 2u : kOut;
+        r[j] = __builtin_amdgcn_raw_buffer_load_b128(arr == 0 ? rs : rb, off, 0, 0);
+      }
+      u32x4* d = reinterpret_cast<u32x4*>(arr == 0 ? ws_s : ws_b);
+#pragma unroll
+      for (int j = 0; j < C::kWL; ++j) {
+        const int i = tid + j * kRpThreads;
+        if (i < RW * kPR) {
+          d[i] = r[j];
+          if (arr == 0) {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) bad |= !fast_scale_ok(r[j][e] & 0xFFFFu) || !fast_scale_ok(r[j][e] >> 16);
+          }
+        }
+      }
+    }
+    return bad;
+  };
+
+  // ---- weights: one phase of the wave's blocks, double-buffered in registers ----
+  u32x4 wv[2][BPW][V];
+  uint32_t wo[BPW];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j) {
+    const int row = r0 + 16 * (wave + kRpWaves * j) + n;
+    wo[j] = (j < nbw) ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
+  }
+  // Piece v of every block of phase ph into register buffer J (a zero-length resource when the
+  // phase does not exist: the loads then read zero without touching memory).
+  auto fetch_v = [&](int J, int v, int ph, bool live) __attribute__((always_inline)) {
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(P.w), 0,
+                                                                        live ? wrec : 0, kBufferRsrcWord3);
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+      wv[J][j][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo[j] + (uint32_t)(v * 64), ph * (C::PH / 2), 0);
+  };
+
+  f32x4 acc[BPW][MB];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j)
+#pragma unroll
+    for (int i = 0; i < MB; ++i) acc[j][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // ---- one phase: LDS stage `st`, register buffer J; piece v of every block is refilled with
+  // phase `nph` (two phases ahead) as soon as super-step v has been used ----
+  auto compute = [&](int st, int pw, auto jc, auto fast, int nph, bool nlive) __attribute__((always_inline)) {
+    constexpr int J = decltype(jc)::value;
+    constexpr bool FAST = decltype(fast)::value;
+    const u32x4* xb = xs(st);
+    // Phase pw of the window: dwords pw * V .. pw * V + V - 1 of each row's window run.
+    const uint32_t* sb32 = reinterpret_cast<const uint32_t*>(ws_s) + pw * V;
+    const uint32_t* bb32 = reinterpret_cast<const uint32_t*>(ws_b) + pw * V;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      // This lane's words of super-step v lie in group 2 v + g / 2 of the phase; dword v of row
+      // (wave + W j) * 16 + n holds groups 2 v and 2 v + 1.
+      float c1[BPW], c2[BPW], bfv[BPW];
+#pragma unroll
+      for (int j = 0; j < BPW; ++j) {
+        const int lrow = 16 * (wave + kRpWaves * j) + n;
+        const uint32_t sd = j < nbw ? sb32[lrow * (C::kWB / 4) + v] : 0u;
+        const uint32_t bd = j < nbw ? bb32[lrow * (C::kWB / 4) + v] : 0u;
+        const uint32_t sbits = (g >> 1) ? (sd >> 16) : (sd & 0xFFFFu);
+        const uint32_t bbits = (g >> 1) ? (bd >> 16) : (bd & 0xFFFFu);
+        const float sf = bf16_to_f32(sbits);
+        bfv[j] = bf16_to_f32(bbits);
+        c1[j] = FAST ? sf * 16777216.0f : sf;
+        c2[j] = FAST ? sf * 1048576.0f : sf * 0.0625f;
+      }
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        u32x4 a[MB];
+#pragma unroll
+        for (int i = 0; i < MB; ++i) a[i] = xb[(v * 16 + g * 4 + t) * MP + i * 16 + n];
+#pragma unroll
+        for (int j = 0; j < BPW; ++j) {
+          if (j < nbw) {
+            const u32x4 B = FAST ? dequant_word_fast(wv[J][j][v][t], c1[j], c2[j], bfv[j])
+                                 : dequant_word(wv[J][j][v][t], c1[j], c2[j], bfv[j]);
+#pragma unroll
+            for (int i = 0; i < MB; ++i)
+              acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(B), acc[j][i], 0, 0, 0);
+          }
+        }
+      }
+      fetch_v(J, v, nph, nlive);
+    }
+  };
+
+  // ---- prologue: scale window of phase pa, x of phases pa and pa + 1, their weights ----
+  stage_load(pa, np > 0);
+#pragma unroll
+  for (int v = 0; v < V; ++v) fetch_v(0, v, pa, np > 0);
+  stage_store(0);
+  stage_load(pa + 1, np > 1);
+#pragma unroll
+  for (int v = 0; v < V; ++v) fetch_v(1, v, pa + 1, np > 1);
+  stage_store(1);
+  // Windows are aligned to absolute phases (WP-phase boundaries of K), so every 16-byte piece of
+  // a window is 16-byte aligned.
+  bool winbad = __syncthreads_or(stage_window(pa - pa % C::WP)) != 0;
+
+  // ---- phase ph from register buffer J and x stage (ph - pa) % 3; phase ph + 2 is loaded
+  // meanwhile (its x into stage (ph - pa + 2) % 3, published by the closing barrier). A phase that
+  // starts a scale window restages the window first (after the previous phase's barrier). ----
+  auto phase = [&](int ph, auto jc) __attribute__((always_inline)) {
+    const int k = ph - pa;
+    const int st = k % 3, st2 = (k + 2) % 3, pw = ph % C::WP;
+    if (pw == 0 && k > 0) winbad = __syncthreads_or(stage_window(ph)) != 0;
+    const bool live2 = ph + 2 < pb;
+    stage_load(ph + 2, live2);  // issued before the refills: the stores below wait for these alone
+    if (!winbad)
+      compute(st, pw, jc, std::true_type{}, ph + 2, live2);
+    else
+      compute(st, pw, jc, std::false_type{}, ph + 2, live2);
+    stage_store(st2);
+    __syncthreads();
+  };
+  int i = 0;
+  for (; i + 2 <= np; i += 2) {
+    phase(pa + i, std::integral_constant<int, 0>{});
+    phase(pa + i + 1, std::integral_constant<int, 1>{});
+  }
+  if (i < np) phase(pa + i, std::integral_constant<int, 0>{});
+
+  // ---- epilogue ----
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+  // bf16 tile of y through LDS: tile[m][local column], then 16-byte row chunks.
+  uint16_t* yt = reinterpret_cast<uint16_t*>(lds);
+  auto write_y = [&]() __attribute__((always_inline)) {
+    // Chunk c = m * (RW / 8) + q holds columns 8 q .. 8 q + 7 of row m.
+    const int cpr = nrows / 8;  // chunks per row
+    for (int c = tid; c < P.M * cpr; c += kRpThreads) {
+      const int m = c / cpr, q = c - m * cpr;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(yt + m * RW + q * 8);
+      __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)m * (uint32_t)P.N + (uint32_t)(r0 + q * 8)) * 2u, 0, 0);
+    }
+  };
+  auto tile_to_lds = [&](const f32x4 (&a)[BPW][MB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int j = 0; j < BPW; ++j) {
+      if (j < nbw) {
+        const int col = 16 * (wave + kRpWaves * j) + n;
+#pragma unroll
+        for (int ii = 0; ii < MB; ++ii)
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int m = ii * 16 + 4 * g + r;
+            yt[m * RW + col] = (uint16_t)(pack_bf16x2(a[j][ii][r], 0.0f) & 0xFFFFu);
+          }
+      }
+    }
+  };
+
+  if (P.S == 1) {
+    tile_to_lds(acc);
+    __syncthreads();
+    write_y();
+    return;
+  }
+
+  // K split: store this workgroup's fp32 partial tile (item (wave, j, i) lane-major), count in,
+  // and let the last workgroup of the range add the partials in workgroup order.
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      P.part, 0, rsrc_bytes((unsigned long long)gridDim.x * C::kItems * 16), kBufferRsrcWord3);
+#pragma unroll
+  for (int j = 0; j < BPW; ++j)
+#pragma unroll
+    for (int ii = 0; ii < MB; ++ii) {
+      const uint32_t item = (uint32_t)(((wave * BPW + j) * MB + ii) * 64 + lane);
+      if (j < nbw)
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[j][ii]), rp,
+                                               ((uint32_t)p * C::kItems + item) * 16u, 0, kCoherent);
+    }
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&P.cnt[range], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    s_last = prev == (uint32_t)(P.S - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (!s_last) return;
+  // Sum the range's partials: each lane its own items, contributors in order, loads in batches.
+  f32x4 sum[BPW][MB];
+#pragma unroll
+  for (int j = 0; j < BPW; ++j)
+#pragma unroll
+    for (int ii = 0; ii < MB; ++ii) sum[j][ii] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  const int q0 = range * P.S;
+  for (int q = 0; q < P.S; ++q) {
+    f32x4 v[BPW][MB];
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+#pragma unroll
+      for (int ii = 0; ii < MB; ++ii) {
+        const uint32_t item = (uint32_t)(((wave * BPW + j) * MB + ii) * 64 + lane);
+        const uint32_t off = j < nbw ? ((uint32_t)(q0 + q) * C::kItems + item) * 16u : kOut;
+        v[j][ii] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kCoherent));
+      }
+#pragma unroll
+    for (int j = 0; j < BPW; ++j)
+#pragma unroll
+      for (int ii = 0; ii < MB; ++ii) {
+        sum[j][ii][0] += v[j][ii][0]; sum[j][ii][1] += v[j][ii][1];
+        sum[j][ii][2] += v[j][ii][2]; sum[j][ii][3] += v[j][ii][3];
+      }
+  }
+  tile_to_lds(sum);
+  __syncthreads();
+  write_y();
+  if (tid == 0) __hip_atomic_store(&P.cnt[range], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+}  // namespace
+
+// Kernel table: id -> (row blocks of x, super-steps per phase, blocks per wave, waves).
+#define QMM4_ROWPHASE_VARIANTS(X) \
+  X(0, 1, 2, 5, 8)                \
+  X(1, 2, 2, 5, 8)                \
+  X(2, 4, 2, 3, 8)                \
+  X(3, 1, 4, 2, 8)                \
+  X(4, 2, 4, 2, 8)                \
+  X(5, 4, 2, 2, 8)                \
+  X(6, 1, 4, 1, 8)                \
+  X(7, 2, 4, 1, 8)                \
+  X(8, 4, 2, 1, 8)
+constexpr int kRpVariants = 9;
+
+#define QMM4_RPCFG(id, mb, v, bpw, w) typedef RpCfg<mb, v, bpw, w> RpCfg##id;
+QMM4_ROWPHASE_VARIANTS(QMM4_RPCFG)
+#undef QMM4_RPCFG
+
+static bool rowphase_geometry(int id, int* mb, int* v, int* bpw, size_t* lds, int* items, int* waves = nullptr) {
+  switch (id) {
+#define QMM4_RPG(i, m, vv, b, w)                                                                     \
+  case i:                                                                                           \
+    *mb = m; *v = vv; *bpw = b; *lds = RpCfg##i::kLds; *items = RpCfg##i::kItems;                    \
+    if (waves) *waves = w;                                                                          \
+    return true;
+    QMM4_ROWPHASE_VARIANTS(QMM4_RPG)
+#undef QMM4_RPG
+    default: return false;
+  }
+}
+
+static const void* rowphase_func(int id) {
+  switch (id) {
+#define QMM4_RPF(i, m, vv, b, w) \
+  case i: return reinterpret_cast<const void*>(&rowphase_kernel<RpCfg##i>);
+    QMM4_ROWPHASE_VARIANTS(QMM4_RPF)
+#undef QMM4_RPF
+    default: return nullptr;
+  }
+}
+
+#ifndef QMM4_RP_NARROW_BPW
+#define QMM4_RP_NARROW_BPW 2  // blocks per wave when K is split
+#endif
+
+bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
+  if (M < 1 || M > 64 || N % 16 != 0 || cus < 1) return false;
+  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  const int NB = N / 16;
+  const int ks = K / 128;
+  // Row offsets of this kernel stay below 2 GiB (rows past the end are addressed at 2 GiB).
+  if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 31)) return false;
+  // Wide: every CU its own rows over all of K (at least one block per wave). Narrow: ranges of
+  // QMM4_RP_NARROW_BPW blocks per wave, K split over the CUs.
+  constexpr int kW = 8;  // waves per workgroup of every variant
+  const bool wide = NB >= kW * cus;
+  const int want = wide ? ((NB + cus - 1) / cus + kW - 1) / kW : QMM4_RP_NARROW_BPW;
+  // The variant for mb rows with the fewest blocks per wave that still holds `want` (or the most).
+  int id = -1, best_b = 0;
+  for (int c = 0; c < kRpVariants; ++c) {
+    int cm, cv, cb, items;
+    size_t l;
+    rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
+    if (cm != mb || ks % cv != 0) continue;
+    const bool fits = cb >= want;
+    const bool best_fits = best_b >= want;
+    if (id < 0 || (fits && (!best_fits || cb < best_b)) || (!fits && !best_fits && cb > best_b)) {
+      id = c;
+      best_b = cb;
+    }
+  }
+  if (id < 0) return false;
+  int cm, v, bpw, items;
+  size_t lds;
+  rowphase_geometry(id, &cm, &v, &bpw, &lds, &items);
+  const int NP = ks / v;
+  int BW, S;
+  if (wide) {
+    BW = (NB + cus - 1) / cus;
+    if (BW > kW * bpw) BW = kW * bpw;
+    S = 1;
+  } else {
+    BW = kW * bpw;
+    const int ranges = (NB + BW - 1) / BW;
+    S = cus / ranges;
+    if (S < 1) S = 1;
+    if (S > NP) S = NP;
+  }
+  plan->variant = id;
+  plan->BW = BW;
+  plan->S = S;
+  plan->NP = NP;
+  plan->ranges = (NB + BW - 1) / BW;
+  plan->blocks = plan->ranges * S;
+  plan->lds = lds;
+  plan->part_bytes = S > 1 ? (size_t)plan->blocks * items * 16 : 0;
+  plan->wide = wide;
+  return true;
+}
+
+hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                           const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
+                           hipStream_t stream) {
+  RowPhaseParams P;
+  P.x = x; P.s = s; P.b = b; P.w = w; P.y = y; P.part = part; P.cnt = cnt;
+  P.M = M; P.N = N; P.K = K;
+  P.NB = N / 16; P.BW = plan.BW; P.S = plan.S; P.NP = plan.NP;
+  const void* f = rowphase_func(plan.variant);
+  if (!f) return hipErrorInvalidValue;
+  hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)plan.lds);
+  if (e != hipSuccess) return e;
+  switch (plan.variant) {
+#define QMM4_RPL(i, m, vv, bb, w)                                                                          \
+  case i:                                                                                                 \
+    hipLaunchKernelGGL(rowphase_kernel<RpCfg##i>, dim3(plan.blocks), dim3(RpCfg##i::kRpThreads), plan.lds, \
+                       stream, P);                                                                        \
+    break;
+    QMM4_ROWPHASE_VARIANTS(QMM4_RPL)
+#undef QMM4_RPL
+    default: return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace qmm4

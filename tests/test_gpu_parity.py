@@ -290,6 +290,45 @@ def test_rowsplit_one_hot_is_exact_dequant(kind):
         assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
 
 
+# ----------------------------------------------------------------------------- row-phase path
+# More than 16 rows (or up to 16 when N gives every wave its own blocks) take the row-phase kernel
+# (K a multiple of 512). Wide shapes give each workgroup whole rows over all of K (N = 16 * 2049
+# leaves the last range a partial one); narrow ones split K over the workgroups of a block range.
+# K = 3072 ends in a partial scale window.
+@pytest.mark.parametrize("m,k,n", [(17, 5120, 4096), (33, 2048, 32784), (8, 5120, 34848), (48, 3072, 33024),
+                                   (64, 1024, 2064), (24, 17408, 1024)])
+def test_rowphase_shapes(m, k, n):
+    note(f"row-phase {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 11 + k + n)
+    check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"row-phase {m}x{k}x{n}", (x, w, s, b))
+
+
+@pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48)])
+@pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
+def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
+    """One-hot rows of x on the row-phase path (wide and K-split): each output is one dequantized
+    weight and must equal the oracle's bit for bit, for scale windows dequantized in the fast
+    form, in the general form, and for a mix of the two."""
+    k = 2048
+    rng = np.random.default_rng({"fast": 21, "mixed": 22, "slow": 23}[kind] + n)
+    s, b = scale_bias_pairs(kind, n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in (0, 1000, k - m):
+        ks = k0 + np.arange(m)
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), ks] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.empty((m, n), dtype=np.uint16)
+        for i, kk in enumerate(ks):
+            g = kk // 64
+            ref[i] = O.dequantize(w[:, 8 * g:8 * g + 8], s[:, g:g + 1], b[:, g:g + 1])[:, kk - 64 * g]
+        keep = (ref & 0x7F80) != 0  # subnormal bf16 weights test the MFMA, not the dequant
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 # ----------------------------------------------------------------------------- host integration
 def test_side_stream_and_workspace_growth():
     cases = [O.make_inputs(16, 5120, 512, seed=1), O.make_inputs(64, 17408, 1024, seed=2), O.make_inputs(3, 256, 64, seed=3)]
