@@ -64,8 +64,11 @@ struct RpCfg {
   static constexpr int kSB = 4 * V;               // bytes of scales (or biases) per row and phase
   static constexpr int WP = 64 / kSB;             // phases per scale window (64 bytes of each row)
   static constexpr int kWB = WP * kSB;            // window bytes per row and array
+  // LDS row stride of a window: 16 bytes of padding put the 16 rows one read touches (one per
+  // lane n) in distinct banks (a 64-byte stride would give four rows per bank).
+  static constexpr int kWS = kWB + 16;
   static constexpr size_t kXBytes = (size_t)kXPieces * 16;
-  static constexpr size_t kWinBytes = (size_t)RW * kWB;  // one array's window
+  static constexpr size_t kWinBytes = (size_t)RW * kWS;  // one array's window
   static constexpr int kStages = 3;  // x stages: phase p in use, p + 1 staged, p + 2 being staged
   static constexpr size_t kYBytes = (size_t)MP * RW * 2;   // epilogue: bf16 tile of y
   static constexpr size_t kMain = kStages * kXBytes + 2 * kWinBytes;
@@ -120,28 +123,25 @@ void rowphase_kernel(RowPhaseParams P) {
   uint8_t* const ws_s = lds + C::kStages * C::kXBytes;  // scale window [RW][kWB]
   uint8_t* const ws_b = ws_s + C::kWinBytes;            // bias window
 
-  // ---- staging of one phase's x pieces ----
+  // ---- staging of one phase's x pieces, global -> LDS directly (no registers) ----
   // x piece i = (v * 16 + g4 * 4 + t) * MP + m holds x[m][PH ph + 128 v + 32 g4 + 8 t .. + 8):
-  // the A fragment of MFMA (v, t) for lane (m, g4). Rows m >= M read as zero.
-  u32x4 xr[C::kXL];
-  auto stage_load = [&](int ph, bool live) __attribute__((always_inline)) {
+  // the A fragment of MFMA (v, t) for lane (m, g4). Rows m >= M read as zero. Wave w's j-th load
+  // fills pieces j * kRpThreads + 64 w .. + 63, one contiguous kilobyte of the stage (the LDS
+  // destination of a lane is the instruction's base + 16 lane). Completion is waited for with an
+  // explicit vector memory count one phase later, before the barrier that publishes the stage.
+  static_assert(C::kXPieces % kRpThreads == 0, "whole x loads per thread");
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  auto stage_x = [&](int st, int ph, bool live) __attribute__((always_inline)) {
 #pragma unroll
     for (int j = 0; j < C::kXL; ++j) {
       const int i = tid + j * kRpThreads;
       const int m = i % MP, q = i / MP;  // q = v * 16 + g4 * 4 + t
       const int v = q >> 4, g4 = (q >> 2) & 3, t = q & 3;
-      const uint32_t off = (live && i < C::kXPieces && m < P.M)
+      const uint32_t off = (live && m < P.M)
                                ? ((uint32_t)m * (uint32_t)P.K + (uint32_t)(ph * C::PH + 128 * v + 32 * g4 + 8 * t)) * 2u
                                : kOut;
-      xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-    }
-  };
-  auto stage_store = [&](int J) __attribute__((always_inline)) {
-    u32x4* xd = xs(J);
-#pragma unroll
-    for (int j = 0; j < C::kXL; ++j) {
-      const int i = tid + j * kRpThreads;
-      if (i < C::kXPieces) xd[i] = xr[j];
+      const lds_ptr dst = (lds_ptr)(reinterpret_cast<uint8_t*>(xs(st)) + (size_t)(j * kRpThreads + 64 * wave) * 16);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, dst, 16, off, 0, 0, 0);
     }
   };
 
@@ -170,7 +170,8 @@ void rowphase_kernel(RowPhaseParams P) {
       for (int j = 0; j < C::kWL; ++j) {
         const int i = tid + j * kRpThreads;
         if (i < RW * kPR) {
-          d[i] = r[j];
+          const int row = i / kPR, pc = i - row * kPR;
+          d[row * (C::kWS / 16) + pc] = r[j];
           if (arr == 0) {
 #pragma unroll
             for (int e = 0; e < 4; ++e) bad |= !fast_scale_ok(r[j][e] & 0xFFFFu) || !fast_scale_ok(r[j][e] >> 16);
@@ -222,8 +223,8 @@ void rowphase_kernel(RowPhaseParams P) {
 #pragma unroll
       for (int j = 0; j < BPW; ++j) {
         const int lrow = 16 * (wave + kRpWaves * j) + n;
-        const uint32_t sd = j < nbw ? sb32[lrow * (C::kWB / 4) + v] : 0u;
-        const uint32_t bd = j < nbw ? bb32[lrow * (C::kWB / 4) + v] : 0u;
+        const uint32_t sd = sb32[lrow * (C::kWS / 4) + v];
+        const uint32_t bd = bb32[lrow * (C::kWS / 4) + v];
         const uint32_t sbits = (g >> 1) ? (sd >> 16) : (sd & 0xFFFFu);
         const uint32_t bbits = (g >> 1) ? (bd >> 16) : (bd & 0xFFFFu);
         const float sf = bf16_to_f32(sbits);
@@ -236,48 +237,54 @@ void rowphase_kernel(RowPhaseParams P) {
         u32x4 a[MB];
 #pragma unroll
         for (int i = 0; i < MB; ++i) a[i] = xb[(v * 16 + g * 4 + t) * MP + i * 16 + n];
+        // Blocks past this wave's count hold zero weights (their loads lie outside the buffer)
+        // and sums that are never stored: computing them keeps the loop free of branches.
 #pragma unroll
         for (int j = 0; j < BPW; ++j) {
-          if (j < nbw) {
-            const u32x4 B = FAST ? dequant_word_fast(wv[J][j][v][t], c1[j], c2[j], bfv[j])
-                                 : dequant_word(wv[J][j][v][t], c1[j], c2[j], bfv[j]);
+          const u32x4 B = FAST ? dequant_word_fast(wv[J][j][v][t], c1[j], c2[j], bfv[j])
+                               : dequant_word(wv[J][j][v][t], c1[j], c2[j], bfv[j]);
 #pragma unroll
-            for (int i = 0; i < MB; ++i)
-              acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(B), acc[j][i], 0, 0, 0);
-          }
+          for (int i = 0; i < MB; ++i)
+            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(B), acc[j][i], 0, 0, 0);
         }
       }
       fetch_v(J, v, nph, nlive);
     }
   };
 
-  // ---- prologue: scale window of phase pa, x of phases pa and pa + 1, their weights ----
-  stage_load(pa, np > 0);
+  // ---- prologue: x of phases pa and pa + 1, their weights, the scale window of phase pa ----
+  stage_x(0, pa, np > 0);
+  stage_x(1, pa + 1, np > 1);
 #pragma unroll
   for (int v = 0; v < V; ++v) fetch_v(0, v, pa, np > 0);
-  stage_store(0);
-  stage_load(pa + 1, np > 1);
 #pragma unroll
   for (int v = 0; v < V; ++v) fetch_v(1, v, pa + 1, np > 1);
-  stage_store(1);
   // Windows are aligned to absolute phases (WP-phase boundaries of K), so every 16-byte piece of
-  // a window is 16-byte aligned.
+  // a window is 16-byte aligned. The window's loads return after the x loads above (the vector
+  // memory count is in order), so its stores also find both x stages written.
   bool winbad = __syncthreads_or(stage_window(pa - pa % C::WP)) != 0;
 
-  // ---- phase ph from register buffer J and x stage (ph - pa) % 3; phase ph + 2 is loaded
-  // meanwhile (its x into stage (ph - pa + 2) % 3, published by the closing barrier). A phase that
-  // starts a scale window restages the window first (after the previous phase's barrier). ----
+  // Loads issued after the x of phase ph + 1 by the end of phase ph: the rest of phase ph - 1's
+  // weight refills, the x of phase ph + 2 and phase ph's refills.
+  constexpr int kAfter = 2 * BPW * V + C::kXL;
+  static_assert(kAfter < 64, "vector memory count range");
+
+  // ---- phase ph from register buffer J and x stage (ph - pa) % 3. Meanwhile phase ph + 2 is
+  // loaded: its x into stage (ph - pa + 2) % 3 (last read in phase ph - 1), its weights into
+  // buffer J as phase ph's pieces are used. A phase that starts a scale window restages the window
+  // first (after the previous phase's barrier). ----
   auto phase = [&](int ph, auto jc) __attribute__((always_inline)) {
     const int k = ph - pa;
     const int st = k % 3, st2 = (k + 2) % 3, pw = ph % C::WP;
     if (pw == 0 && k > 0) winbad = __syncthreads_or(stage_window(ph)) != 0;
     const bool live2 = ph + 2 < pb;
-    stage_load(ph + 2, live2);  // issued before the refills: the stores below wait for these alone
+    stage_x(st2, ph + 2, live2);
     if (!winbad)
       compute(st, pw, jc, std::true_type{}, ph + 2, live2);
     else
       compute(st, pw, jc, std::false_type{}, ph + 2, live2);
-    stage_store(st2);
+    // The x of phase ph + 1 (issued at the start of phase ph - 1) is in LDS; publish it.
+    asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter) : "memory");
     __syncthreads();
   };
   int i = 0;
