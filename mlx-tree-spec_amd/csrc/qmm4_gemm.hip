@@ -5,11 +5,12 @@
 // BN x BK block is dequantized once to bf16 (qmm_packed.py:629-637) into LDS and multiplied with
 // the BM x BK activation block; accumulation in fp32; bf16 out.
 //
-// Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 8 waves in a 2 x 4
-// arrangement (two waves per SIMD, so one wave's loads and LDS traffic overlap the other's MFMAs),
-// each wave a 128 x 64 block of 4 x 2 MFMA 32x32x16 tiles (128 fp32 accumulators per lane). LDS
-// holds two stages of [256][64 + 8] bf16 for the activations and for the dequantized weights
-// (147 KB).
+// Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 4 waves in a 2 x 2
+// arrangement (one per SIMD), each wave a 128 x 128 block of 4 x 4 MFMA 32x32x16 tiles (256 fp32
+// accumulators per lane). The larger wave tile reads each activation and weight fragment from LDS
+// for four MFMAs, so a K step moves 128 KB out of LDS instead of the 192 KB of 128 x 64 wave
+// tiles: LDS bandwidth, not the matrix cores, bounded the smaller tiles. LDS holds two stages of
+// [256][64 + 8] bf16 for the activations and for the dequantized weights (147 KB).
 //
 // Pipeline: the raw inputs of a K step (activation chunks, packed codes, scale and bias) are loaded
 // into registers two steps ahead of their use, through buffer resources (rows past M and columns
@@ -30,7 +31,12 @@ namespace qmm4 {
 namespace {
 
 constexpr int BK = 64, LDK = BK + 8;  // K step; LDS row pitch (bf16) of a K step
-constexpr int kThreads = 512;
+#ifndef QMM4_GEMM_WAVES
+#define QMM4_GEMM_WAVES 8
+#endif
+constexpr int kWaves = QMM4_GEMM_WAVES;  // 4: a 2 x 2 wave grid; 8: 2 x 4
+constexpr int kThreads = 64 * kWaves;
+constexpr int kWavesN = kWaves / 2;
 constexpr int kGroupM = 4;
 constexpr int kTile = 256;            // the grid's tile; tail launches cut a tile into 128 x 128 quarters
 
@@ -48,26 +54,30 @@ struct GemmParams {
 
 template <int BM, int BN>
 struct GemmCfg {
-  static constexpr int WM = BM / 2, WN = BN / 4;  // wave tile (2 x 4 waves)
-  static constexpr int I = WM / 32, J = WN / 32;  // MFMA 32x32 blocks per wave
-  static constexpr int AJ = BM / 64;              // activation chunks per thread per step
-  static constexpr int WPT = BN / 64;             // code words per thread per step
-  static constexpr int TPC = 8 / WPT;             // threads per weight column
-  static constexpr int LDC = BN + 8;              // LDS row pitch (bf16) of the output tile
+  static constexpr int WM = BM / 2, WN = BN / kWavesN;  // wave tile (2 x kWavesN waves)
+  static constexpr int I = WM / 32, J = WN / 32;        // MFMA 32x32 blocks per wave
+  static constexpr int RPP = kThreads / 8;              // activation rows per load pass
+  static constexpr int AJ = BM / RPP;                   // activation chunks per thread per step
+  static constexpr int WPT = BN * 8 / kThreads;         // code words per thread per step
+  static constexpr int TPC = 8 / WPT;                   // threads per weight column
+  static constexpr int WV = (WPT + 3) / 4;              // 16-byte word vectors per thread
+  static constexpr int LDC = BN + 8;                    // LDS row pitch (bf16) of the output tile
   static constexpr size_t kSmem = (size_t)2 * (BM + BN) * LDK * sizeof(uint16_t);
   static_assert((size_t)BM * LDC * sizeof(uint16_t) <= kSmem, "output tile fits the K-step stages");
-  static_assert(I >= 1 && J >= 1 && (WPT == 2 || WPT == 4) && AJ % 2 == 0, "tile shape");
+  static_assert(I >= 1 && J >= 1 && (WPT == 2 || WPT == 4 || WPT == 8) && AJ % 2 == 0, "tile shape");
 };
 
 // One K step's raw inputs held by a thread.
 template <class C>
 struct Raw {
-  u32x4 a[C::AJ];  // activations: rows a_r0 + 64 j of the tile, 16-byte chunk a_kc of the step
-  u32x4 w;         // code words WPT * b_part .. + WPT - 1 of column n0 + b_col
-  uint32_t s, b;   // that group's scale and bias (bf16 bits)
+  u32x4 a[C::AJ];     // activations: rows a_r0 + RPP j of the tile, 16-byte chunk a_kc of the step
+  u32x4 w[C::WV];     // code words WPT * b_part .. + WPT - 1 of column n0 + b_col
+  uint32_t s, b;      // that group's scale and bias (bf16 bits)
 };
 
-template <int BM, int BN>
+// SB8: scales and biases are loaded 8 groups (8 K steps) at a time with one 16-byte load per
+// column (K % 512 == 0); otherwise one 2-byte load per K step.
+template <int BM, int BN, bool SB8>
 __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   using C = GemmCfg<BM, BN>;
   constexpr int I = C::I, J = C::J, AJ = C::AJ, WPT = C::WPT, LDC = C::LDC;
@@ -78,7 +88,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave >> 2, wn = wave & 3;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
 
   // Tile: XCD-contiguous remap of full-tile launches, then a grouped row-major walk of the
   // 256 x 256 tiles; a quarter launch gives each tile's four 128 x 128 quarters to four workgroups.
@@ -116,7 +126,7 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int a_kc = tid & 7;
   const int a_r0 = tid >> 3;
   const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
-  const int xrow64 = 64 * P.K * 2;
+  const int xrowp = C::RPP * P.K * 2;  // byte distance of consecutive load passes
   const int b_col = tid / C::TPC, b_part = tid % C::TPC;
   const uint32_t col = (uint32_t)(n0 + b_col);
   const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)(b_part * WPT * 4);
@@ -128,35 +138,62 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
     const int k = kt < nk ? kt : nk - 1;
 #pragma unroll
     for (int j = 0; j < AJ; ++j)
-      R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrow64, 0);
-    if constexpr (WPT == 4) {
-      R.w = __builtin_amdgcn_raw_buffer_load_b128(rw, woff, k * 32, 0);
+      R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrowp, 0);
+    if constexpr (WPT >= 4) {
+#pragma unroll
+      for (int v = 0; v < C::WV; ++v) R.w[v] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff + v * 16, k * 32, 0);
     } else {
       const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rw, woff, k * 32, 0);
-      R.w = u32x4{t.x, t.y, 0u, 0u};
+      R.w[0] = u32x4{t.x, t.y, 0u, 0u};
     }
-    R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
-    R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
+    if constexpr (!SB8) {
+      R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
+      R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
+    }
+  };
+  // SB8: groups 8 q .. 8 q + 7 of this thread's column; scur holds the block of the step being
+  // written to LDS, snext the following block (loaded 3 steps before it is first needed).
+  u32x4 scur = {0u, 0u, 0u, 0u}, bcur = scur, snext = scur, bnext = scur;
+  auto load_sb8 = [&](int kt, u32x4& s8, u32x4& b8) __attribute__((always_inline)) {
+    const int k = kt < nk ? kt : 0;
+    s8 = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 2, 0);
+    b8 = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 2, 0);
+  };
+  // Group kt % 8 of a block: dword (kt % 8) / 2, half kt % 2 (wave-uniform selects).
+  auto pick = [&](const u32x4& v, int kt) __attribute__((always_inline)) {
+    const int d = (kt >> 1) & 3;
+    const uint32_t w = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+    return (kt & 1) ? (w >> 16) : (w & 0xFFFFu);
+  };
+  // Scale and bias bits of step kt for the weight stores.
+  auto sb_of = [&](const Raw<C>& R, int kt, uint32_t& sb, uint32_t& bb) __attribute__((always_inline)) {
+    if constexpr (SB8) {
+      sb = pick(scur, kt);
+      bb = pick(bcur, kt);
+    } else {
+      sb = R.s & 0xFFFFu;
+      bb = R.b & 0xFFFFu;
+    }
   };
   auto store_a = [&](const Raw<C>& R, int st, int j0, int j1) {
     uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
 #pragma unroll
-    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + 64 * j * LDK) = R.a[j];
+    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + C::RPP * j * LDK) = R.a[j];
   };
-  auto store_b_fast = [&](const Raw<C>& R, int st, int j0, int j1) {
+  auto store_b_fast = [&](const Raw<C>& R, int st, int j0, int j1, uint32_t sbits, uint32_t bbits) {
     uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
-    const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
+    const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
     const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
 #pragma unroll
     for (int j = j0; j < j1; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j], s24, s20, bf);
+      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j >> 2][j & 3], s24, s20, bf);
   };
-  auto store_b_exact = [&](const Raw<C>& R, int st) {
+  auto store_b_exact = [&](const Raw<C>& R, int st, uint32_t sbits, uint32_t bbits) {
     uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
-    const float sf = bf16_to_f32(R.s & 0xFFFFu), bf = bf16_to_f32(R.b & 0xFFFFu);
+    const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
 #pragma unroll
     for (int j = 0; j < WPT; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j], sf, sf * 0.0625f, bf);
+      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
   };
 
   f32x16 acc[I][J];
@@ -175,29 +212,46 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   auto step = [&](int kt, auto parity) {
     constexpr int ST = decltype(parity)::value;
     Raw<C>& R = raw[ST ^ 1];
+    if constexpr (SB8) {
+      // Step kt + 1 starts a block of 8 groups: move to it.
+      if (((kt + 1) & 7) == 0) {
+        scur = snext;
+        bcur = bnext;
+      }
+    }
+    uint32_t sbits, bbits;
+    sb_of(R, kt + 1, sbits, bbits);
     const uint16_t* as = As + ST * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
     const uint16_t* bs = Bs + ST * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
-#pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      bf16x8 Af[I], Bf[J];
+    // Fragments are double-buffered across the four 16-k sub-steps: sub-step ks + 1's reads are
+    // issued before sub-step ks's MFMAs, so LDS latency hides behind them.
+    bf16x8 Af[2][I], Bf[2][J];
+    auto frags = [&](int ks, int sl) __attribute__((always_inline)) {
 #pragma unroll
       for (int i = 0; i < I; ++i)
-        Af[i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
+        Af[sl][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
 #pragma unroll
       for (int j = 0; j < J; ++j)
-        Bf[j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
+        Bf[sl][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
+    };
+    frags(0, 0);
+#pragma unroll
+    for (int ks = 0; ks < BK / 16; ++ks) {
+      if (ks + 1 < BK / 16) frags(ks + 1, (ks + 1) & 1);
 #pragma unroll
       for (int i = 0; i < I; ++i)
 #pragma unroll
-        for (int j = 0; j < J; ++j) acc[i][j] = Mfma<32>::mma(Af[i], Bf[j], acc[i][j]);
+        for (int j = 0; j < J; ++j) acc[i][j] = Mfma<32>::mma(Af[ks & 1][i], Bf[ks & 1][j], acc[i][j]);
       if (ks == 0) store_a(R, ST ^ 1, 0, AJ / 2);
       if (ks == 1) store_a(R, ST ^ 1, AJ / 2, AJ);
-      if (ks == 2) store_b_fast(R, ST ^ 1, 0, WPT / 2);
-      if (ks == 3) store_b_fast(R, ST ^ 1, WPT / 2, WPT);
+      if (ks == 2) store_b_fast(R, ST ^ 1, 0, WPT / 2, sbits, bbits);
+      if (ks == 3) store_b_fast(R, ST ^ 1, WPT / 2, WPT, sbits, bbits);
     }
-    if (!fast_scale_ok(R.s)) store_b_exact(R, ST ^ 1);
+    if (!fast_scale_ok(sbits)) store_b_exact(R, ST ^ 1, sbits, bbits);
     __syncthreads();
     load(kt + 3, R);
+    if constexpr (SB8)
+      if (((kt + 3) & 7) == 0) load_sb8(kt + 3, snext, bnext);
     // Keep these loads right behind the barrier (the scheduler would sink them toward their use two
     // steps later, into the middle of the next step's MFMAs).
     __builtin_amdgcn_sched_barrier(0);
@@ -206,9 +260,14 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   // Prologue: steps 0 and 1 in registers, step 0 in LDS, step 2 in flight.
   load(0, raw[0]);
   load(1, raw[1]);
-  store_a(raw[0], 0, 0, AJ);
-  store_b_fast(raw[0], 0, 0, WPT);
-  if (!fast_scale_ok(raw[0].s)) store_b_exact(raw[0], 0);
+  if constexpr (SB8) load_sb8(0, scur, bcur);
+  {
+    uint32_t sbits, bbits;
+    sb_of(raw[0], 0, sbits, bbits);
+    store_a(raw[0], 0, 0, AJ);
+    store_b_fast(raw[0], 0, 0, WPT, sbits, bbits);
+    if (!fast_scale_ok(sbits)) store_b_exact(raw[0], 0, sbits, bbits);
+  }
   load(2, raw[0]);
   __syncthreads();
 
@@ -247,17 +306,17 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   }
 }
 
-template <int BM, int BN>
+template <int BM, int BN, bool SB8>
 hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
-  static bool attr_set = false;
+  constexpr size_t smem = GemmCfg<BM, BN>::kSmem;
+  static bool attr_set = false;  // the attribute is per function; setting it twice is harmless
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)GemmCfg<BM, BN>::kSmem);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, SB8>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  constexpr size_t smem = GemmCfg<BM, BN>::kSmem;
-  hipLaunchKernelGGL((gemm_kernel<BM, BN>), dim3(blocks), dim3(kThreads), smem, stream, P);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SB8>), dim3(blocks), dim3(kThreads), smem, stream, P);
   return hipGetLastError();
 }
 
@@ -278,16 +337,20 @@ hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s, 
   const int rem = total % c;
   const int tail = (rem > 0 && 4 * rem <= 2 * c) ? rem : 0;
   const int main_tiles = total - tail;
+  // 16-byte loads of 8 groups need 16-byte aligned scale rows and pointers.
+  const bool sb8 = K % 512 == 0 && (reinterpret_cast<uintptr_t>(s) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0;
   if (main_tiles > 0) {
     P.tile0 = 0;
     P.quarter = 0;
-    hipError_t e = launch_tiles<256, 256>(P, main_tiles, stream);
+    hipError_t e = sb8 ? launch_tiles<256, 256, true>(P, main_tiles, stream)
+                       : launch_tiles<256, 256, false>(P, main_tiles, stream);
     if (e != hipSuccess) return e;
   }
   if (tail > 0) {
     P.tile0 = main_tiles;
     P.quarter = 1;
-    hipError_t e = launch_tiles<128, 128>(P, 4 * tail, stream);
+    hipError_t e = sb8 ? launch_tiles<128, 128, true>(P, 4 * tail, stream)
+                       : launch_tiles<128, 128, false>(P, 4 * tail, stream);
     if (e != hipSuccess) return e;
   }
   return hipSuccess;
