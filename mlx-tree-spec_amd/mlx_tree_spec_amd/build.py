@@ -50,7 +50,8 @@ def build(verbose: bool = False) -> str:
         with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
             list(ex.map(_compile, srcs, objs))
         out_tmp = LIB_PATH + f".tmp{os.getpid()}"
-        cmd = ["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", out_tmp]
+        # --no-undefined: a kernel whose host stub the compiler dropped fails here, not at load time.
+        cmd = ["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *objs, "-o", out_tmp]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
