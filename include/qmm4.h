@@ -54,6 +54,25 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
                      int transpose, void* hip_stream);
 
 /*
+ * y = silu(x @ dequant(w_gate)^T) * (x @ dequant(w_up)^T) — a fused gate+up projection with the
+ * SiLU·mul epilogue, the input of down_proj in the MLP of the verify forward
+ * (src/mlx_tree_spec/tree_verify.py:446: layer.mlp(x) = down_proj(silu(gate_proj(x)) * up_proj(x));
+ * config "decode GEMV, fused gate+up projection"). Replaces the two quantized-matmul calls plus the
+ * elementwise silu and multiply.
+ *   w = [w_gate; w_up]: uint32 [N, K/8], gate rows 0 .. N/2 - 1, up rows N/2 .. N - 1; scales and
+ *   biases bf16 [N, K/group_size] in the same row order; y: bf16 [M, N/2].
+ *   The gate and up sums are rounded to bf16 (the values the two projections would store), then
+ *   out = bf16(bf16(g * bf16(sigmoid(g))) * u), one rounding per operation of the unfused
+ *   composition. Same requirements as qmm4_affine_bf16, plus N % 32 == 0 and y 16-byte aligned.
+ *   Up to 4 rows over a large N run as one kernel; otherwise the projection goes to a
+ *   library-held [M, N] buffer (per device and stream, grown on demand) and the epilogue is a
+ *   second pass. Deterministic.
+ */
+int qmm4_gate_up_silu_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                           void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                           int transpose, void* hip_stream);
+
+/*
  * out = dequant(w) as bf16 [N, K] — the bit-exact unpack + affine dequant.
  * Replaces mx.dequantize(w, scales, biases, group_size=64, bits=4) as used by the reference's
  * exact-reference definition (tests/test_units.py:108) and qmm_packed.py:200-201 / 635-636.

@@ -107,6 +107,38 @@ int get_workspace(int dev, hipStream_t stream, size_t counter_bytes, size_t part
   return QMM4_OK;
 }
 
+// Scratch for one (device, stream) that an entry point fills and reads back in the same call (the
+// gate+up projection before its separate epilogue pass). Grown on demand; the old buffer is freed
+// once the stream has finished with it.
+struct Scratch {
+  void* base = nullptr;
+  size_t bytes = 0;
+};
+std::map<std::pair<int, hipStream_t>, Scratch> g_scratch;
+
+int get_scratch(int dev, hipStream_t stream, size_t bytes, void** out) {
+  Scratch& sc = g_scratch[std::make_pair(dev, stream)];
+  if (sc.base == nullptr || sc.bytes < bytes) {
+    const size_t nb = std::max(sc.bytes, (bytes + 255) / 256 * 256);
+    if (sc.base != nullptr) {
+      hipError_t e = hipStreamSynchronize(stream);
+      if (e != hipSuccess) return hip_fail(e, "hipStreamSynchronize");
+      (void)hipFree(sc.base);
+      sc = Scratch();
+    }
+    void* p = nullptr;
+    hipError_t e = hipMalloc(&p, nb);
+    if (e != hipSuccess) {
+      (void)hipGetLastError();
+      return fail(QMM4_ERR_NOMEM, "scratch allocation of %zu bytes failed: %s", nb, hipGetErrorString(e));
+    }
+    sc.base = p;
+    sc.bytes = nb;
+  }
+  *out = sc.base;
+  return QMM4_OK;
+}
+
 int check_format(int group_size, int bits, int transpose) {
   if (bits != 4) return fail(QMM4_ERR_UNSUPPORTED, "bits=%d: only 4-bit codes are supported", bits);
   if (group_size != 64)
@@ -116,6 +148,11 @@ int check_format(int group_size, int bits, int transpose) {
                 transpose);
   return QMM4_OK;
 }
+
+int check_qmm_args(const void* x, const uint32_t* w, const void* scales, const void* biases, const void* y,
+                   int64_t M, int64_t N, int64_t K, int group_size, int bits, int transpose);
+int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, const void* scales,
+                 const void* biases, void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream);
 
 }  // namespace
 
@@ -129,6 +166,68 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
                      void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
                      int transpose, void* hip_stream) {
   g_last_error.clear();
+  int rc = check_qmm_args(x, w, scales, biases, y, M, N, K, group_size, bits, transpose);
+  if (rc || M == 0 || N == 0) return rc;
+  hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceInfo* di = nullptr;
+  rc = device_info(dev, &di);
+  if (rc) return rc;
+  return dispatch_qmm(dev, di, x, w, scales, biases, y, M, N, K, stream);
+}
+
+int qmm4_gate_up_silu_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                           void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                           int transpose, void* hip_stream) {
+  g_last_error.clear();
+  int rc = check_qmm_args(x, w, scales, biases, y, M, N, K, group_size, bits, transpose);
+  if (rc) return rc;
+  if (N % 32 != 0)
+    return fail(QMM4_ERR_INVALID, "N=%lld must be a multiple of 32 (gate and up halves of whole 16-row blocks)",
+                (long long)N);
+  if (M == 0 || N == 0) return QMM4_OK;
+  if (!aligned(y, 16)) return fail(QMM4_ERR_INVALID, "y must be 16-byte aligned");
+  hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  std::lock_guard<std::mutex> lock(g_mu);
+  DeviceInfo* di = nullptr;
+  rc = device_info(dev, &di);
+  if (rc) return rc;
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  const uint16_t* sb = static_cast<const uint16_t*>(scales);
+  const uint16_t* bb = static_cast<const uint16_t*>(biases);
+  uint16_t* yb = static_cast<uint16_t*>(y);
+#ifndef QMM4_NO_ROWSPLIT
+  // Decode rows: the row-split kernel with the epilogue fused (one launch, no [M, N] round trip).
+  qmm4::RowSplitPlan rplan;
+  if (qmm4::rowsplit_plan((int)M, (int)N, (int)K, di->cus, true, &rplan)) {
+    e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
+    if (e != hipSuccess) return hip_fail(e, "fused gate+up row-split kernel launch");
+    return QMM4_OK;
+  }
+#endif
+  // Otherwise the projection into a library-held [M, N] buffer, then the epilogue as its own pass.
+  void* t = nullptr;
+  rc = get_scratch(dev, stream, (size_t)M * (size_t)N * sizeof(uint16_t), &t);
+  if (rc) return rc;
+  rc = dispatch_qmm(dev, di, x, w, scales, biases, t, M, N, K, stream);
+  if (rc) return rc;
+  e = qmm4::launch_silu_mul(static_cast<const uint16_t*>(t), yb, (int)M, (int)(N / 2), stream);
+  if (e != hipSuccess) return hip_fail(e, "silu-mul kernel launch");
+  return QMM4_OK;
+}
+
+}  // extern "C"
+
+namespace {
+
+int check_qmm_args(const void* x, const uint32_t* w, const void* scales, const void* biases, const void* y,
+                   int64_t M, int64_t N, int64_t K, int group_size, int bits, int transpose) {
   int rc = check_format(group_size, bits, transpose);
   if (rc) return rc;
   if (M < 0 || N < 0 || K <= 0)
@@ -155,20 +254,18 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
       (unsigned long long)(M + 256) * (unsigned long long)N * 2 >= (1ULL << 32))
     return fail(QMM4_ERR_INVALID, "x [%lld, %lld] or y [%lld, %lld] exceeds 4 GiB", (long long)M,
                 (long long)K, (long long)M, (long long)N);
+  return QMM4_OK;
+}
 
-  hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+// The kernel choice for y = x @ dequant(w)^T (arguments already checked, M and N > 0, g_mu held).
+int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, const void* scales,
+                 const void* biases, void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream) {
   const uint16_t* xb = static_cast<const uint16_t*>(x);
   const uint16_t* sb = static_cast<const uint16_t*>(scales);
   const uint16_t* bb = static_cast<const uint16_t*>(biases);
   uint16_t* yb = static_cast<uint16_t*>(y);
-
-  int dev = 0;
-  hipError_t e = hipGetDevice(&dev);
-  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
-  std::lock_guard<std::mutex> lock(g_mu);
-  DeviceInfo* di = nullptr;
-  rc = device_info(dev, &di);
-  if (rc) return rc;
+  hipError_t e;
+  int rc;
 
   if (M > 64) {
     e = qmm4::launch_gemm(xb, w, sb, bb, yb, (int)M, (int)N, (int)K, di->cus, stream);
@@ -179,7 +276,7 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
 #ifndef QMM4_NO_ROWSPLIT
   // Up to 4 rows and enough output columns to give every CU its own rows: the row-split kernel.
   qmm4::RowSplitPlan rplan;
-  if (qmm4::rowsplit_plan((int)M, (int)N, (int)K, di->cus, &rplan)) {
+  if (qmm4::rowsplit_plan((int)M, (int)N, (int)K, di->cus, false, &rplan)) {
     e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
     if (e != hipSuccess) return hip_fail(e, "row-split kernel launch");
     return QMM4_OK;
@@ -275,6 +372,10 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
   if (e != hipSuccess) return hip_fail(e, "skinny kernel launch");
   return QMM4_OK;
 }
+
+}  // namespace
+
+extern "C" {
 
 int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
                          int64_t N, int64_t K, int group_size, int bits, void* hip_stream) {

@@ -39,6 +39,20 @@ __device__ __forceinline__ uint32_t pack_bf16x2(float a, float b) {
   return __builtin_bit_cast(uint32_t, r);
 }
 
+__device__ __forceinline__ uint32_t bf16_rne(float a) { return pack_bf16x2(a, 0.0f) & 0xFFFFu; }
+
+// silu(g) * u on bf16 operands, one bf16 rounding per operation as the unfused MLP computes it
+// (silu(x) = x * sigmoid(x), then the product with up; every intermediate a bf16 array):
+//   s = bf16(sigmoid(g)), t = bf16(g * s), out = bf16(t * u),
+// with sigmoid(g) = 1 / (1 + exp(-g)) in fp32 (exp(-g) overflowing to infinity gives 0; the
+// complement form 1 - sigmoid(|g|) would cancel for g < -10).
+__device__ __forceinline__ uint32_t silu_mul_bf16(uint32_t gbits, uint32_t ubits) {
+  const float g = bf16_to_f32(gbits);
+  const float sg = 1.0f / (1.0f + expf(-g));
+  const float t = bf16_to_f32(bf16_rne(g * bf16_to_f32(bf16_rne(sg))));
+  return bf16_rne(t * bf16_to_f32(ubits));
+}
+
 // Dequantize one packed word (codes for k = 8c .. 8c+7) with its group's scale and bias.
 // Result dword j holds bf16 for k = 8c+2j (low half) and 8c+2j+1 (high half).
 //

@@ -78,16 +78,22 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
 // Row-split decode kernel (up to 4 rows, output columns split evenly over one workgroup per CU).
 struct RowSplitPlan {
   int V;        // super-steps (128 k) per unit
-  int R;        // weight rows per workgroup
-  int RB;       // 16-row blocks per workgroup
+  bool fused;   // fused gate+up: y = silu(x w_gate^T) * (x w_up^T), w = [w_gate; w_up]
+  int Nout;     // output columns (N, or N / 2 when fused)
+  int R;        // output columns per workgroup
+  int RB;       // 16-row blocks per workgroup: ceil(R / 16), or ceil(2R / 16) when fused
   int SU;       // units per block (K / (128 V))
   int blocks;   // workgroups
   size_t smem;  // dynamic LDS bytes
 };
-// Fills `plan` and returns true when the shape suits the row-split kernel on `cus` CUs.
-bool rowsplit_plan(int M, int N, int K, int cus, RowSplitPlan* plan);
+// Fills `plan` and returns true when the shape suits the row-split kernel on `cus` CUs. N is the
+// number of weight rows (for the fused gate+up, both halves).
+bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan);
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream);
+
+// y[m, j] = silu_mul_bf16(t[m, j], t[m, n + j]) for t bf16 [M, 2n] (the unfused gate+up epilogue).
+hipError_t launch_silu_mul(const uint16_t* t, uint16_t* y, int M, int n, hipStream_t stream);
 
 // Zero n uint32 words (the skinny kernel's arrival counters when their workspace is allocated).
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);

@@ -28,6 +28,12 @@
 //    g = 0 hold x rows 0..3, so a slot is 16 lanes x 16 bytes. After one barrier the workgroup adds
 //    the slots of each block in step order (deterministic whatever wave ran which unit) and
 //    writes bf16 y.
+//  * Fused gate+up (FUSED): w is [w_gate; w_up] (N rows, up rows from N / 2), y is [M, N / 2] =
+//    silu(x @ w_gate^T) * (x @ w_up^T). Workgroup p owns output columns [p R, p R + R); its 2R
+//    weight rows are listed gate rows first, then the up rows of the same columns (N / 2 further),
+//    and cut into 16-row blocks (one block may hold both). Each column's gate and up sums are
+//    formed exactly as above, rounded to bf16 (the values the unfused projection would store), and
+//    combined by silu_mul_bf16.
 #include <type_traits>
 
 #include "qmm4_common.h"
@@ -50,9 +56,10 @@ struct RowSplitParams {
   const uint16_t* b;
   uint16_t* y;
   int M, N, K;
-  int R;   // weight rows per workgroup (a multiple of 8)
-  int RB;  // 16-row blocks per workgroup, ceil(R / 16)
-  int SU;  // units per block, K / (128 V)
+  int Nout;  // output columns: N, or N / 2 for the fused gate+up
+  int R;     // output columns per workgroup (a multiple of 4)
+  int RB;    // 16-row blocks per workgroup: ceil(R / 16), or ceil(2R / 16) for the fused gate+up
+  int SU;    // units per block, K / (128 V)
 };
 
 template <int V>
@@ -80,7 +87,7 @@ __device__ __forceinline__ Scales<V> load_scales(__amdgpu_buffer_rsrc_t r, uint3
 __host__ __device__ inline size_t rowsplit_xs_bytes(int K) { return (size_t)(K >> 7) * 16 * kRsMP * 16; }
 __host__ __device__ inline size_t rowsplit_part_bytes(int units) { return (size_t)units * 16 * 16; }
 
-template <int V>
+template <int V, bool FUSED>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -98,7 +105,7 @@ void rowsplit_kernel(RowSplitParams P) {
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
   const int r0 = blockIdx.x * P.R;
-  const int r1 = min(P.N, r0 + P.R);
+  const int r1 = min(P.Nout, r0 + P.R);
   const int KG = P.K >> 6;
 
   // x pieces: item i = sq * M + m is the 16-byte piece sq (k = 8 sq .. 8 sq + 7) of row m, stored
@@ -154,9 +161,13 @@ void rowsplit_kernel(RowSplitParams P) {
     const bool live = u < U;
     const int uu = live ? u : 0;
     const int b = uu / SU, st = uu - b * SU;
-    const int row = r0 + b * 16 + n;
-    const uint32_t wo = row < r1 ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
-    const uint32_t so = row < r1 ? (uint32_t)row * (uint32_t)KG * 2u : kOut;
+    // Output column of this lane's row, and the weight row (the up half sits N / 2 further).
+    const int lrow = b * 16 + n;
+    const bool up = FUSED && lrow >= P.R;
+    const int col = r0 + (up ? lrow - P.R : lrow);
+    const int row = col + (up ? P.Nout : 0);
+    const uint32_t wo = col < r1 ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
+    const uint32_t so = col < r1 ? (uint32_t)row * (uint32_t)KG * 2u : kOut;
     const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint32_t*>(P.w), 0, live ? wrec : 0, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
@@ -243,38 +254,52 @@ void rowsplit_kernel(RowSplitParams P) {
   }
   __syncthreads();
 
-  // y[m, row] = sum over the block's steps, in step order, of its unit slots; lane element m of a
-  // slot is x row m.
+  // y[m, col] = sum over the block's steps, in step order, of its unit slots; lane element m of a
+  // slot is x row m. Fused: the same for the column's gate and up blocks, then silu * up.
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
-      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
-  for (int idx = tid; idx < P.RB * 16; idx += kRsThreads) {
-    const int b = idx >> 4, nn = idx & 15;
-    const int row = r0 + b * 16 + nn;
-    if (row >= r1) continue;
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.Nout * 2), kBufferRsrcWord3);
+  auto row_sum = [&](int lrow) __attribute__((always_inline)) {
+    const int b = lrow >> 4, nn = lrow & 15;
     f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
     for (int st = 0; st < SU; ++st) {
       const f32x4 c = part[(b * SU + st) * 16 + nn];
       sum[0] += c[0]; sum[1] += c[1]; sum[2] += c[2]; sum[3] += c[3];
     }
+    return sum;
+  };
+  for (int c = tid; c < P.R; c += kRsThreads) {
+    const int col = r0 + c;
+    if (col >= r1) continue;
+    const f32x4 sum = row_sum(c);
+    if constexpr (FUSED) {
+      const f32x4 sup = row_sum(P.R + c);
 #pragma unroll
-    for (int m = 0; m < kRsMP; ++m)
-      if (m < P.M)
-        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16x2(sum[m], 0.0f) & 0xFFFFu), ry,
-                                              (uint32_t)(m * P.N + row) * 2u, 0, 0);
+      for (int m = 0; m < kRsMP; ++m)
+        if (m < P.M)
+          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)silu_mul_bf16(bf16_rne(sum[m]), bf16_rne(sup[m])), ry,
+                                                (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
+    } else {
+#pragma unroll
+      for (int m = 0; m < kRsMP; ++m)
+        if (m < P.M)
+          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_rne(sum[m]), ry, (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
+    }
   }
 }
 
 }  // namespace
 
-bool rowsplit_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
+bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan) {
   if (M < 1 || M > kRsMP || cus < 1) return false;
+  if (fused && N % 32 != 0) return false;
   const int S = K >> 7;
   // Units of 4 super-steps (256 bytes of a row: two whole 128-byte lines) where K allows: a unit
   // boundary inside a line splits it between two waves' fetches.
   const int V = S % 4 == 0 ? 4 : S % 5 == 0 ? 5 : 0;
   if (V == 0) return false;
-  const int R = ((N + cus - 1) / cus + 7) / 8 * 8;
-  const int RB = (R + 15) / 16;
+  const int nout = fused ? N / 2 : N;
+  const int R = ((nout + cus - 1) / cus + 3) / 4 * 4;
+  const int RB = ((fused ? 2 * R : R) + 15) / 16;
   const int SU = S / V;
   // At least 4 blocks per workgroup (the decomposition only pays when rows alone fill the GPU).
   if (RB < 4) return false;
@@ -283,12 +308,27 @@ bool rowsplit_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
   // Row offsets of this kernel stay below 1 GiB.
   if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 30)) return false;
   plan->V = V;
+  plan->fused = fused;
+  plan->Nout = nout;
   plan->R = R;
   plan->RB = RB;
   plan->SU = SU;
-  plan->blocks = (N + R - 1) / R;
+  plan->blocks = (nout + R - 1) / R;
   plan->smem = smem;
   return true;
+}
+
+template <int V, bool FUSED>
+hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
+  static bool attr_set = false;
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rowsplit_kernel<V, FUSED>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL((rowsplit_kernel<V, FUSED>), dim3(plan.blocks), dim3(kRsThreads), plan.smem, stream, P);
+  return hipGetLastError();
 }
 
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
@@ -296,21 +336,10 @@ hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const ui
   RowSplitParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
-  P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
-  const void* f = plan.V == 5 ? reinterpret_cast<const void*>(&rowsplit_kernel<5>)
-                              : reinterpret_cast<const void*>(&rowsplit_kernel<4>);
-  static bool attr_set[2] = {false, false};
-  const int vi = plan.V == 5 ? 1 : 0;
-  if (!attr_set[vi]) {
-    hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
-    if (e != hipSuccess) return e;
-    attr_set[vi] = true;
-  }
-  if (plan.V == 5)
-    hipLaunchKernelGGL(rowsplit_kernel<5>, dim3(plan.blocks), dim3(kRsThreads), plan.smem, stream, P);
-  else
-    hipLaunchKernelGGL(rowsplit_kernel<4>, dim3(plan.blocks), dim3(kRsThreads), plan.smem, stream, P);
-  return hipGetLastError();
+  P.Nout = plan.Nout; P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
+  if (plan.fused)
+    return plan.V == 5 ? launch_rowsplit_t<5, true>(plan, P, stream) : launch_rowsplit_t<4, true>(plan, P, stream);
+  return plan.V == 5 ? launch_rowsplit_t<5, false>(plan, P, stream) : launch_rowsplit_t<4, false>(plan, P, stream);
 }
 
 }  // namespace qmm4

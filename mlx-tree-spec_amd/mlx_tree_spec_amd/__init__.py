@@ -6,11 +6,11 @@ All compute runs in libqmm4.so (hand-written HIP kernels, C ABI in include/qmm4.
 this package does not load it, the first call does, and fails loudly if it is not built.
 """
 
-from .packed_linear import STATS, QuantizedLinear, eligible, install
-from .qmm import dequantize, pack_nax, quantized_matmul, unpack_nax
+from .packed_linear import STATS, QuantizedLinear, QuantizedMLP, eligible, install
+from .qmm import dequantize, gate_up_silu, pack_nax, quantized_matmul, unpack_nax
 
 __all__ = [
-    "quantized_matmul", "dequantize", "pack_nax", "unpack_nax",
-    "QuantizedLinear", "eligible", "install", "STATS",
+    "quantized_matmul", "gate_up_silu", "dequantize", "pack_nax", "unpack_nax",
+    "QuantizedLinear", "QuantizedMLP", "eligible", "install", "STATS",
 ]
 __version__ = "0.1.0"

@@ -27,7 +27,7 @@ from collections import defaultdict
 import torch
 
 from . import _lib
-from .qmm import quantized_matmul
+from .qmm import gate_up_silu, quantized_matmul
 
 SKINNY_MAX_ROWS = 64  # rows <= this take the skinny kernel (the reference's PREFILL_M is 64)
 STATS: dict[str, int] = defaultdict(int)
@@ -69,6 +69,37 @@ class QuantizedLinear(torch.nn.Module):
 
     def forward(self, x: torch.Tensor) -> torch.Tensor:
         return _call(self, x)
+
+
+class QuantizedMLP(torch.nn.Module):
+    """down_proj(silu(gate_proj(x)) * up_proj(x)) over MLX-format 4-bit linears, with gate and up
+    fused into one projection whose epilogue applies silu * up (tree_verify.py:446, layer.mlp).
+
+    The gate and up weights (and their scales and biases) are stacked once, gate rows first, so a
+    call is one gate_up_silu (one kernel for up to 4 rows) and one down_proj matmul.
+    """
+
+    def __init__(self, gate_proj: QuantizedLinear, up_proj: QuantizedLinear, down_proj: QuantizedLinear):
+        super().__init__()
+        for name, m in (("gate_proj", gate_proj), ("up_proj", up_proj), ("down_proj", down_proj)):
+            if not eligible(m):
+                raise ValueError(f"[QuantizedMLP] {name} is not an eligible 4-bit affine QuantizedLinear")
+        if gate_proj.weight.shape != up_proj.weight.shape or gate_proj.group_size != up_proj.group_size:
+            raise ValueError("[QuantizedMLP] gate_proj and up_proj must have the same shape and group size")
+        if down_proj.input_dims != gate_proj.output_dims or down_proj.output_dims != gate_proj.input_dims:
+            raise ValueError(f"[QuantizedMLP] down_proj {down_proj.input_dims}->{down_proj.output_dims} does not "
+                             f"match gate/up {gate_proj.input_dims}->{gate_proj.output_dims}")
+        self.group_size = gate_proj.group_size
+        self.register_buffer("gate_up_weight", torch.cat([gate_proj.weight, up_proj.weight], 0).contiguous())
+        self.register_buffer("gate_up_scales", torch.cat([gate_proj.scales, up_proj.scales], 0).contiguous())
+        self.register_buffer("gate_up_biases", torch.cat([gate_proj.biases, up_proj.biases], 0).contiguous())
+        self.down_proj = down_proj
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        STATS["gate_up_silu"] += 1
+        h = gate_up_silu(x, self.gate_up_weight, self.gate_up_scales, self.gate_up_biases,
+                         group_size=self.group_size)
+        return self.down_proj(h)
 
 
 def eligible(mod) -> bool:

@@ -94,6 +94,40 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     return y
 
 
+def gate_up_silu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
+                 group_size: int = 64, bits: int = 4, mode: str = "affine") -> torch.Tensor:
+    """silu(x @ dequant(w_gate).T) * (x @ dequant(w_up).T) for w = [w_gate; w_up] (N rows, gate
+    first): the fused gate+up projection and SiLU·mul of an MLP, bf16 (..., N/2) (HIP kernels).
+
+    Same value as splitting quantized_matmul(x, w, ...) into halves g, u and computing
+    bf16(bf16(g * bf16(sigmoid(g))) * u) elementwise, the unfused composition of
+    tree_verify.py:446's layer.mlp (down_proj(silu(gate_proj(x)) * up_proj(x))) up to down_proj.
+    """
+    _check_format(group_size, bits, True, mode)
+    if x.dtype != torch.bfloat16:
+        raise ValueError(f"[gate_up_silu] x must be bfloat16, got {x.dtype}")
+    if x.dim() < 1:
+        raise ValueError("[gate_up_silu] x must have at least one dimension")
+    k = x.shape[-1]
+    n, _ = _check_weights(w, scales, biases, k, group_size, bits, "gate_up_silu")
+    if n % 32:
+        raise ValueError(f"[gate_up_silu] w has {n} rows; gate and up halves need a multiple of 32")
+    dev = _check_device("gate_up_silu", x, w, scales, biases)
+    x2 = _contig(x.reshape(-1, k))
+    m = x2.shape[0]
+    w = _contig(w)
+    scales = scales.contiguous()
+    biases = biases.contiguous()
+    y = torch.empty((*x.shape[:-1], n // 2), dtype=torch.bfloat16, device=dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        stream = torch.cuda.current_stream(dev).cuda_stream
+        rc = lib.qmm4_gate_up_silu_bf16(x2.data_ptr(), w.data_ptr(), scales.data_ptr(), biases.data_ptr(),
+                                        y.data_ptr(), m, n, k, group_size, bits, 1, stream)
+    _lib.check(rc, "gate_up_silu")
+    return y
+
+
 def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = 64,
                bits: int = 4, mode: str = "affine") -> torch.Tensor:
     """bf16 [N, K] with w_deq = bf16_rne(fp32(s) * q + fp32(b)), bit-exact (HIP kernel)."""

@@ -108,6 +108,30 @@ def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: i
     return f32_to_bf16_bits(y.astype(np.float32))
 
 
+# ----------------------------------------------------------------------------- MLP epilogue
+def silu_mul(g, u) -> np.ndarray:
+    """bf16 bits of silu(g) * u for bf16 bits g, u, one bf16 rounding per operation as the unfused
+    MLP evaluates it on bf16 arrays (tree_verify.py:446: down_proj(silu(gate_proj(x)) *
+    up_proj(x)); silu(x) = x * sigmoid(x)):  s = bf16(sigmoid(g)), t = bf16(g * s), bf16(t * u).
+    sigmoid is evaluated in fp32 as 1 / (1 + exp(-g)). (MLX's own kernels for these elementwise
+    ops are not in the reference: their last-ulp rounding of the sigmoid is parity unpinned; this
+    restatement fixes one.)"""
+    gf = bf16_bits_to_f32(g)
+    with np.errstate(over="ignore"):
+        sg = (np.float32(1.0) / (np.float32(1.0) + np.exp(-gf))).astype(np.float32)
+    s = bf16_bits_to_f32(f32_to_bf16_bits(sg))
+    t = bf16_bits_to_f32(f32_to_bf16_bits(gf * s))
+    return f32_to_bf16_bits(t * bf16_bits_to_f32(u))
+
+
+def gate_up_silu(x, w, scales, biases, group_size: int = GROUP_SIZE, bits: int = BITS) -> np.ndarray:
+    """bf16 bits [M, N/2] of silu(x @ w_gate.T) * (x @ w_up.T), w = [w_gate; w_up]: each half rounded
+    to bf16 as its own projection would store it, then silu_mul."""
+    y = quantized_matmul(x, w, scales, biases, True, group_size, bits)
+    h = y.shape[-1] // 2
+    return silu_mul(y[..., :h], y[..., h:])
+
+
 # ----------------------------------------------------------------------------- metrics
 def max_rel(y, ref) -> float:
     """max|y - ref| / max|ref| (experiments/qmm_prefill.py:98)."""

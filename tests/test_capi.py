@@ -20,8 +20,8 @@ def declared_functions():
 
 
 def test_header_declares_expected_api():
-    assert declared_functions() == sorted(["qmm4_affine_bf16", "dequant4_affine_bf16", "qmm4_last_error",
-                                           "qmm4_abi_version"])
+    assert declared_functions() == sorted(["qmm4_affine_bf16", "qmm4_gate_up_silu_bf16", "dequant4_affine_bf16",
+                                           "qmm4_last_error", "qmm4_abi_version"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -61,6 +61,31 @@ def test_qmm_empty_is_noop():
     assert call(M=0, ptr=0) == _lib.QMM4_OK
     assert call(N=0, ptr=0) == _lib.QMM4_OK
     assert _lib.last_error() == ""
+
+
+def call_gate_up(M=4, N=64, K=128, gs=64, bits=4, transpose=1, ptr=0x10000, y=0x20000):
+    lib = _lib.load()
+    return lib.qmm4_gate_up_silu_bf16(ptr, ptr, ptr, ptr, y, M, N, K, gs, bits, transpose, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(bits=2), _lib.QMM4_ERR_UNSUPPORTED, "bits=2"),
+    (dict(gs=128), _lib.QMM4_ERR_UNSUPPORTED, "group_size=128"),
+    (dict(transpose=0), _lib.QMM4_ERR_UNSUPPORTED, "transpose=0"),
+    (dict(K=64), _lib.QMM4_ERR_INVALID, "K=64"),
+    (dict(N=48), _lib.QMM4_ERR_INVALID, "multiple of 32"),
+    (dict(N=24), _lib.QMM4_ERR_INVALID, "N=24"),
+    (dict(ptr=0), _lib.QMM4_ERR_INVALID, "null pointer"),
+    (dict(y=0x20008), _lib.QMM4_ERR_INVALID, "y must be 16-byte aligned"),
+])
+def test_gate_up_rejects(kw, code, msg):
+    assert call_gate_up(**kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_gate_up_empty_is_noop():
+    assert call_gate_up(M=0, ptr=0) == _lib.QMM4_OK
+    assert call_gate_up(N=0, ptr=0) == _lib.QMM4_OK
 
 
 def test_dequant_rejects():

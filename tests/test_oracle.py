@@ -13,7 +13,12 @@ How each oracle function is pinned:
   pack_nax / unpack_nax      index-loop fixture of qmm_packed.py:224-231; round trip
   metrics, byte/flop counts  closed forms (the workload table's published byte counts)
   C restatement (cpu.py)     against the numpy oracle (bit-exact dequant, tolerance on y)
-A planted mistake in the oracle (reversed nibble order, raw-code accumulation) must fail.
+  silu_mul                   closed forms (g = 0, u = 0, saturated g); every bf16 g in [-30, 30]
+                             against g * sigmoid(g) * u in float64 (three roundings: 3 ulps);
+                             torch's own bf16 silu and multiply (within 3 ulps, mostly equal)
+  gate_up_silu               halves of quantized_matmul, gate first, through silu_mul
+A planted mistake in the oracle (reversed nibble order, raw-code accumulation, a sigmoid of the
+wrong sign) must fail.
 """
 
 import numpy as np
@@ -151,6 +156,70 @@ def test_planted_mistakes_fail():
     assert O.mean_rel(raw_bf16, ref) > O.MEAN_REL_TOL
     good = O.bf16_bits_to_f32(O.quantized_matmul(x, w, s, b))
     assert O.mean_rel(good, ref) < O.MEAN_REL_TOL and O.max_rel(good, ref) < O.MAX_REL_TOL
+
+
+def bf16_grid(lo: float, hi: float) -> np.ndarray:
+    """Every finite bf16 bit pattern whose value lies in [lo, hi]."""
+    u = np.arange(1 << 16, dtype=np.uint32).astype(np.uint16)
+    v = O.bf16_bits_to_f32(u)
+    return u[np.isfinite(v) & (v >= lo) & (v <= hi)]
+
+
+def silu_f64(g, u):
+    gf = O.bf16_bits_to_f32(g).astype(np.float64)
+    return gf / (1.0 + np.exp(-gf)) * O.bf16_bits_to_f32(u).astype(np.float64)
+
+
+def within_ulps(out_bits, exact, ulps):
+    """|out - exact| <= ulps bf16 ulps of exact (or of the smallest normal, near zero)."""
+    out = O.bf16_bits_to_f32(out_bits).astype(np.float64)
+    mag = np.maximum(np.abs(exact), 2.0 ** -126)
+    ulp = 2.0 ** (np.floor(np.log2(mag)) - 7)
+    return np.abs(out - exact) <= ulps * ulp
+
+
+def test_silu_mul_closed_forms():
+    one, half = O.f32_to_bf16_bits(np.float32(1.0)), O.f32_to_bf16_bits(np.float32(0.5))
+    g = bf16_grid(-30, 30)
+    assert np.all(O.bf16_bits_to_f32(O.silu_mul(np.zeros(5, np.uint16), g[:5])) == 0)  # silu(0) = 0
+    assert np.all(O.bf16_bits_to_f32(O.silu_mul(g, np.zeros_like(g))) == 0)
+    big = O.f32_to_bf16_bits(np.array([20.0, 64.0, 1000.0], np.float32))  # sigmoid = 1 in fp32
+    assert np.array_equal(O.silu_mul(big, np.full(3, one)), big)
+    assert np.array_equal(O.silu_mul(big, np.full(3, half)), O.f32_to_bf16_bits(O.bf16_bits_to_f32(big) * 0.5))
+    # silu(g) - silu(-g) = g (sigmoid(g) + sigmoid(-g) = 1)
+    gp = bf16_grid(0.5, 8)
+    sp = O.bf16_bits_to_f32(O.silu_mul(gp, np.full(gp.shape, one))).astype(np.float64)
+    sn = O.bf16_bits_to_f32(O.silu_mul(gp ^ np.uint16(0x8000), np.full(gp.shape, one))).astype(np.float64)
+    np.testing.assert_allclose(sp - sn, O.bf16_bits_to_f32(gp), rtol=2 ** -6, atol=2 ** -6)
+
+
+def test_silu_mul_matches_float64_and_torch():
+    g = bf16_grid(-30, 30)
+    for uval in (1.0, -0.75, 3.5):
+        u = np.full(g.shape, O.f32_to_bf16_bits(np.float32(uval)))
+        out = O.silu_mul(g, u)
+        assert within_ulps(out, silu_f64(g, u), 3).all()
+        # torch: silu in fp32 rounded once to bf16, then the bf16 product (one rounding fewer than
+        # the op-by-op composition, which rounds the sigmoid first)
+        tg = torch.from_numpy(g.astype(np.int16)).view(torch.bfloat16)
+        tu = torch.from_numpy(u.astype(np.int16)).view(torch.bfloat16)
+        tref = (torch.nn.functional.silu(tg) * tu).view(torch.int16).numpy().view(np.uint16)
+        assert within_ulps(out, O.bf16_bits_to_f32(tref).astype(np.float64), 3).all()
+        assert np.mean(out == tref) > 0.9
+    # planted mistake: the sigmoid of the wrong sign
+    gf = O.bf16_bits_to_f32(g)
+    wrong = O.f32_to_bf16_bits(gf * (1.0 / (1.0 + np.exp(gf))))
+    assert not within_ulps(wrong, silu_f64(g, np.full(g.shape, O.f32_to_bf16_bits(np.float32(1.0)))), 3).all()
+
+
+def test_gate_up_silu_is_halves_of_the_projection():
+    x, w, s, b = O.make_inputs(3, 256, 64, seed=9)
+    y = O.quantized_matmul(x, w, s, b)
+    h = O.gate_up_silu(x, w, s, b)
+    assert h.shape == (3, 32)
+    assert np.array_equal(h, O.silu_mul(y[:, :32], y[:, 32:]))
+    # gate first: swapping the halves changes the result
+    assert not np.array_equal(h, O.silu_mul(y[:, 32:], y[:, :32]))
 
 
 def test_pack_nax_matches_index_loops():
