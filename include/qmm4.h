@@ -81,6 +81,20 @@ int qmm4_gate_up_silu_bf16(const void* x, const uint32_t* w, const void* scales,
 int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
                          int64_t N, int64_t K, int group_size, int bits, void* hip_stream);
 
+/*
+ * (h, n) = (x + r, rmsnorm(x + r) * weight) — the residual add fused with the RMS norm that follows
+ * it, the op in front of each quantized matmul of the verify forward. Replaces
+ * fused_ops.add_rms_norm(x, r, norm) (src/mlx_tree_spec/fused_ops.py:107-160; called at
+ * tree_verify.py:444-446).
+ *   x, r, h_out, n_out: bf16 [rows, D]; weight: bf16 [D]; per row
+ *     h = bf16(x + r), n = bf16(weight * bf16(h * inv)), inv = 1 / sqrt(sum(h * h) / D + eps),
+ *   the sum in fp32 (its order, like the reference's simdgroup reduction, is the kernel's own).
+ *   Requires rows >= 0, D % 8 == 0, D <= 16384, eps finite and >= 0, every pointer 16-byte
+ *   aligned. rows == 0 is a no-op.
+ */
+int qmm4_add_rms_norm_bf16(const void* x, const void* r, const void* weight, void* h_out, void* n_out,
+                           int64_t rows, int64_t D, float eps, void* hip_stream);
+
 /* Message for the last non-zero return on this host thread ("" if none). */
 const char* qmm4_last_error(void);
 

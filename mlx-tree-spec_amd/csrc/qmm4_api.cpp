@@ -377,6 +377,26 @@ int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, cons
 
 extern "C" {
 
+int qmm4_add_rms_norm_bf16(const void* x, const void* r, const void* weight, void* h_out, void* n_out,
+                           int64_t rows, int64_t D, float eps, void* hip_stream) {
+  g_last_error.clear();
+  if (rows < 0 || D <= 0 || D % 8 != 0 || D > qmm4::add_rms_norm_max_d())
+    return fail(QMM4_ERR_INVALID, "invalid shape rows=%lld D=%lld (D must be a positive multiple of 8, at most %d)",
+                (long long)rows, (long long)D, qmm4::add_rms_norm_max_d());
+  if (rows > (1LL << 30)) return fail(QMM4_ERR_INVALID, "rows=%lld exceeds 2^30", (long long)rows);
+  if (!(eps >= 0.0f) || eps > 1e30f) return fail(QMM4_ERR_INVALID, "eps must be finite and >= 0");
+  if (rows == 0) return QMM4_OK;
+  if (!x || !r || !weight || !h_out || !n_out) return fail(QMM4_ERR_INVALID, "null pointer argument");
+  if (!aligned(x, 16) || !aligned(r, 16) || !aligned(weight, 16) || !aligned(h_out, 16) || !aligned(n_out, 16))
+    return fail(QMM4_ERR_INVALID, "x, r, weight, h_out and n_out must be 16-byte aligned");
+  hipError_t e = qmm4::launch_add_rms_norm(static_cast<const uint16_t*>(x), static_cast<const uint16_t*>(r),
+                                           static_cast<const uint16_t*>(weight), static_cast<uint16_t*>(h_out),
+                                           static_cast<uint16_t*>(n_out), (int)rows, (int)D, eps,
+                                           static_cast<hipStream_t>(hip_stream));
+  if (e != hipSuccess) return hip_fail(e, "add-rms-norm kernel launch");
+  return QMM4_OK;
+}
+
 int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
                          int64_t N, int64_t K, int group_size, int bits, void* hip_stream) {
   g_last_error.clear();

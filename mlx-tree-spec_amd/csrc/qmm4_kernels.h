@@ -95,6 +95,12 @@ hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const ui
 // y[m, j] = silu_mul_bf16(t[m, j], t[m, n + j]) for t bf16 [M, 2n] (the unfused gate+up epilogue).
 hipError_t launch_silu_mul(const uint16_t* t, uint16_t* y, int M, int n, hipStream_t stream);
 
+// h = bf16(x + r), n = bf16(w * bf16(h / sqrt(mean(h^2) + eps))) per row of D (D % 8 == 0,
+// D <= add_rms_norm_max_d(); all pointers 16-byte aligned).
+int add_rms_norm_max_d();
+hipError_t launch_add_rms_norm(const uint16_t* x, const uint16_t* r, const uint16_t* w, uint16_t* h,
+                               uint16_t* n, int rows, int D, float eps, hipStream_t stream);
+
 // Zero n uint32 words (the skinny kernel's arrival counters when their workspace is allocated).
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 

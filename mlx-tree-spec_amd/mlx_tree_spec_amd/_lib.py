@@ -25,6 +25,7 @@ SIGNATURES = {
     "qmm4_affine_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "qmm4_gate_up_silu_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "dequant4_affine_bf16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp]),
+    "qmm4_add_rms_norm_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
     "qmm4_last_error": (ctypes.c_char_p, []),
     "qmm4_abi_version": (_int, []),
 }

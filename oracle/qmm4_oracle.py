@@ -108,6 +108,24 @@ def quantized_matmul(x, w, scales, biases, transpose: bool = True, group_size: i
     return f32_to_bf16_bits(y.astype(np.float32))
 
 
+# ----------------------------------------------------------------------------- residual + RMS norm
+def add_rms_norm(x, r, weight, eps: float):
+    """bf16 bits (h, n), each [rows, D], of the residual add fused with the RMS norm after it
+    (fused_ops.py:107-128): h = bf16(x + r); inv = 1 / sqrt(sum(h*h) / D + eps);
+    n = bf16(w * bf16(h * inv)). The row sum is taken in float64 and rounded to fp32 (the
+    reference's own fp32 summation order, a simdgroup reduction, is not reproducible: its last bit
+    is parity unpinned); the mean, sqrt and reciprocal are correctly rounded fp32 operations."""
+    x = np.asarray(x, dtype=np.uint16)
+    d = x.shape[-1]
+    h = f32_to_bf16_bits(bf16_bits_to_f32(x) + bf16_bits_to_f32(r))
+    hf = bf16_bits_to_f32(h)
+    ss = (hf.astype(np.float64) ** 2).sum(-1).astype(np.float32)
+    inv = (np.float32(1.0) / np.sqrt(ss / np.float32(d) + np.float32(eps))).astype(np.float32)
+    nh = f32_to_bf16_bits(hf * inv[..., None])
+    n = f32_to_bf16_bits(bf16_bits_to_f32(weight) * bf16_bits_to_f32(nh))
+    return h, n
+
+
 # ----------------------------------------------------------------------------- MLP epilogue
 def silu_mul(g, u) -> np.ndarray:
     """bf16 bits of silu(g) * u for bf16 bits g, u, one bf16 rounding per operation as the unfused

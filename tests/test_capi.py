@@ -21,7 +21,7 @@ def declared_functions():
 
 def test_header_declares_expected_api():
     assert declared_functions() == sorted(["qmm4_affine_bf16", "qmm4_gate_up_silu_bf16", "dequant4_affine_bf16",
-                                           "qmm4_last_error", "qmm4_abi_version"])
+                                           "qmm4_add_rms_norm_bf16", "qmm4_last_error", "qmm4_abi_version"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -81,6 +81,26 @@ def call_gate_up(M=4, N=64, K=128, gs=64, bits=4, transpose=1, ptr=0x10000, y=0x
 def test_gate_up_rejects(kw, code, msg):
     assert call_gate_up(**kw) == code
     assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("rows,d,eps,ptr,msg", [
+    (4, 12, 1e-6, 0x10000, "multiple of 8"),
+    (4, 0, 1e-6, 0x10000, "invalid shape"),
+    (4, 16392, 1e-6, 0x10000, "at most 16384"),
+    (-1, 64, 1e-6, 0x10000, "invalid shape"),
+    (4, 64, -1.0, 0x10000, "eps"),
+    (4, 64, float("nan"), 0x10000, "eps"),
+    (4, 64, 1e-6, 0, "null pointer"),
+    (4, 64, 1e-6, 0x10008, "16-byte aligned"),
+])
+def test_add_rms_norm_rejects(rows, d, eps, ptr, msg):
+    lib = _lib.load()
+    assert lib.qmm4_add_rms_norm_bf16(ptr, ptr, ptr, ptr, ptr, rows, d, eps, None) == _lib.QMM4_ERR_INVALID
+    assert msg in _lib.last_error()
+
+
+def test_add_rms_norm_empty_is_noop():
+    assert _lib.load().qmm4_add_rms_norm_bf16(0, 0, 0, 0, 0, 0, 64, 1e-6, None) == _lib.QMM4_OK
 
 
 def test_gate_up_empty_is_noop():

@@ -212,6 +212,49 @@ def test_silu_mul_matches_float64_and_torch():
     assert not within_ulps(wrong, silu_f64(g, np.full(g.shape, O.f32_to_bf16_bits(np.float32(1.0)))), 3).all()
 
 
+def test_add_rms_norm_closed_forms():
+    d = 64
+    one = O.f32_to_bf16_bits(np.float32(1.0))
+    w = O.f32_to_bf16_bits(np.linspace(-2, 2, d).astype(np.float32))
+    # a constant power-of-two row with eps = 0: h = c, inv = 1/|c| exactly, n = sign(c) * w
+    for c in (4.0, -0.5):
+        x = np.full((1, d), O.f32_to_bf16_bits(np.float32(c)))
+        h, n = O.add_rms_norm(x, np.zeros_like(x), w, 0.0)
+        assert np.array_equal(h, x)
+        assert np.array_equal(O.bf16_bits_to_f32(n), np.sign(c) * O.bf16_bits_to_f32(w)[None, :])
+    # h = x + r exactly where it is representable; a zero row gives n = 0 (inv = 1/sqrt(eps))
+    x = np.full((2, d), one)
+    r = np.full((2, d), O.f32_to_bf16_bits(np.float32(-1.0)))
+    h, n = O.add_rms_norm(x, r, w, 1e-6)
+    assert np.all(O.bf16_bits_to_f32(h) == 0) and np.all(O.bf16_bits_to_f32(n) == 0)
+    # eps enters the mean: a row of ones with eps = 3 has inv = 1/2
+    h, n = O.add_rms_norm(np.full((1, d), one), np.zeros((1, d), np.uint16), np.full(d, one), 3.0)
+    assert np.all(O.bf16_bits_to_f32(n) == 0.5)
+
+
+def test_add_rms_norm_matches_torch():
+    rng = np.random.default_rng(3)
+    rows, d, eps = 7, 5120, 1e-6
+    x = O.f32_to_bf16_bits(rng.standard_normal((rows, d)).astype(np.float32))
+    r = O.f32_to_bf16_bits(rng.standard_normal((rows, d)).astype(np.float32) * 0.3)
+    w = O.f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+    h, n = O.add_rms_norm(x, r, w, eps)
+    tb = lambda a: torch.from_numpy(a.astype(np.int16)).view(torch.bfloat16)
+    th = tb(x) + tb(r)  # torch adds bf16 in fp32 and rounds once
+    assert np.array_equal(h, th.view(torch.int16).numpy().view(np.uint16))
+    hf = th.float()
+    normed = (hf * torch.rsqrt(hf.pow(2).mean(-1, keepdim=True) + eps)).to(torch.bfloat16)
+    tn = (tb(w) * normed).view(torch.int16).numpy().view(np.uint16)
+    assert within_ulps(n, O.bf16_bits_to_f32(tn).astype(np.float64), 1).all()
+    assert np.mean(n == tn) >= 0.999
+    # planted mistake: the mean over D + 1 values (inv off by 1e-4 relative) moves ~1% of outputs
+    hf64 = O.bf16_bits_to_f32(h).astype(np.float64)
+    inv = 1.0 / np.sqrt((hf64 ** 2).sum(-1) / (d + 1) + eps)
+    wrong = O.f32_to_bf16_bits((O.bf16_bits_to_f32(w)[None] * O.bf16_bits_to_f32(
+        O.f32_to_bf16_bits((hf64 * inv[:, None]).astype(np.float32)))).astype(np.float32))
+    assert np.mean(wrong == tn) < 0.999
+
+
 def test_gate_up_silu_is_halves_of_the_projection():
     x, w, s, b = O.make_inputs(3, 256, 64, seed=9)
     y = O.quantized_matmul(x, w, s, b)
