@@ -102,6 +102,80 @@ class Workload:
         return sum(bytes_per_call(m, self.k, self.n) for m in self.rows)
 
 
+def time_graph(torch, call, reps: int = 20, replays: int = 5) -> float:
+    """Kernel time per call (s) without host dispatch: `reps` calls captured into a HIP graph,
+    replayed `replays` times between one event pair. call(i, stream) enqueues call i on `stream`
+    (it must not allocate: each op was called once before capture)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        for i in range(3):
+            call(i, side.cuda_stream)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        st = torch.cuda.current_stream().cuda_stream
+        for i in range(reps):
+            call(i, st)
+    g.replay()
+    torch.cuda.synchronize()
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record()
+    for _ in range(replays):
+        g.replay()
+    b.record()
+    torch.cuda.synchronize()
+    return a.elapsed_time(b) * 1e-3 / (replays * reps)
+
+
+def measure_fused(torch, lib, dev, wl: Workload) -> dict:
+    """The ops either side of the projection: the fused gate+up with its SiLU·mul epilogue on the c1
+    weights (the gate and up projections stacked), and the residual add + RMS norm at the model
+    width for decode (4 rows) and a prefill chunk (4096 rows). Timed as graph replays of 20
+    back-to-back calls on rotating inputs (no host dispatch in the figure). HBM-bound; bytes are the
+    algorithmic ones (weights, scales and biases, x, y; for the norm x, r, h, n and the weight row)."""
+    out = {}
+    n2 = wl.n // 2
+    for m in wl.rows:
+        y = torch.empty((m, n2), dtype=torch.int16, device=dev)
+
+        def call(i, stream, m=m, y=y):
+            c = i % wl.copies
+            rc = lib.qmm4_gate_up_silu_bf16(wl.x.data_ptr(), wl.w[c].data_ptr(), wl.s[c].data_ptr(),
+                                            wl.b[c].data_ptr(), y.data_ptr(), m, wl.n, wl.k, 64, 4, 1, stream)
+            if rc != 0:
+                raise RuntimeError(f"qmm4_gate_up_silu_bf16 failed ({rc}): {lib.qmm4_last_error().decode()}")
+
+        med = time_graph(torch, call)
+        byt = wl.n * wl.k // 2 + 4 * wl.n * (wl.k // 64) + 2 * m * wl.k + 2 * m * n2
+        out[f"gate_up_silu M={m}"] = {"us": round(med * 1e6, 2), "gbs": round(byt / med / 1e9, 1),
+                                      "hbm_frac": round(byt / med / 1e9 / HBM_PEAK_GBS, 4), "bytes": byt}
+        log(f"[bench]   gate_up_silu M={m}: {med * 1e6:8.2f} us  {byt / med / 1e9:7.1f} GB/s")
+    d = wl.k
+    g = torch.Generator(device="cpu").manual_seed(3)
+    w = (1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16).to(dev)
+    for rows in (4, 4096):
+        copies = max(2, int(np.ceil(ROTATE_BYTES / (8 * rows * d))))
+        xs = [torch.randn(rows, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(min(copies, 8))]
+        rs = [torch.randn(rows, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(len(xs))]
+        h, nn = torch.empty_like(xs[0]), torch.empty_like(xs[0])
+
+        def call(i, stream, rows=rows, xs=xs, rs=rs, h=h, nn=nn):
+            c = i % len(xs)
+            rc = lib.qmm4_add_rms_norm_bf16(xs[c].data_ptr(), rs[c].data_ptr(), w.data_ptr(), h.data_ptr(),
+                                            nn.data_ptr(), rows, d, 1e-6, stream)
+            if rc != 0:
+                raise RuntimeError(f"qmm4_add_rms_norm_bf16 failed ({rc}): {lib.qmm4_last_error().decode()}")
+
+        med = time_graph(torch, call)
+        byt = 8 * rows * d + 2 * d
+        out[f"add_rms_norm rows={rows} D={d}"] = {"us": round(med * 1e6, 2), "gbs": round(byt / med / 1e9, 1),
+                                                  "hbm_frac": round(byt / med / 1e9 / HBM_PEAK_GBS, 4), "bytes": byt}
+        log(f"[bench]   add_rms_norm {rows}x{d}: {med * 1e6:8.2f} us  {byt / med / 1e9:7.1f} GB/s")
+    return out
+
+
 def time_launches(torch, wl: Workload, m: int, samples: int) -> list[float]:
     """Per-launch kernel time (s) from HIP event pairs on the launch stream."""
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
@@ -225,6 +299,8 @@ def main() -> int:
             torch.cuda.empty_cache()
 
     wl, res = head
+    log("[bench] fused ops either side of the projection")
+    fused = measure_fused(torch, lib, dev, wl)
     # Timed region: exactly K steps, synchronized on both sides.
     for _ in range(args.warmup):
         wl.step()
@@ -273,10 +349,12 @@ def main() -> int:
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qmm4::rowsplit_kernel<4> (rows <= 4, one workgroup per CU owning 136 weight rows)",
+                     "kernel": "qmm4::rowsplit_kernel<4, false> (rows <= 4, one workgroup per CU owning 136 weight "
+                               "rows)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
                      "bytes_per_launch": round(statistics.mean(byts))},
         "workloads": out_workloads,
+        "fused": fused,
     }
     if not args.no_cpu:
         log("[bench] cpu baseline")
