@@ -176,6 +176,59 @@ def measure_fused(torch, lib, dev, wl: Workload) -> dict:
     return out
 
 
+def measure_layer_tail(torch, dev, rows_list=(4, 64), n_layers: int = 2, samples: int = 20) -> dict:
+    """The MLP half of n_layers decoder layers at the model's sizes (D = 5120, H = 17408: the c1 gate+up
+    and c2 down projection shapes), per forward: eager calls from Python against one replay of the
+    same layers captured in a HIP graph. Random weights; the same layers for every sample."""
+    from mlx_tree_spec_amd import GraphedTail, MLPLayer, QuantizedLinear, QuantizedMLP, stack_tail
+
+    d, h = 5120, 17408
+    g = torch.Generator(device="cpu").manual_seed(11)
+
+    def lin(n, k):
+        w = torch.randint(-2 ** 31, 2 ** 31 - 1, (n, k // 8), generator=g, dtype=torch.int32)
+        s = (torch.rand(n, k // 64, generator=g) * 0.004 + 1e-4).to(torch.bfloat16)
+        b = (-8 * s.float() + 1e-3 * torch.randn(n, k // 64, generator=g)).to(torch.bfloat16)
+        return QuantizedLinear.from_quantized(w.to(dev), s.to(dev), b.to(dev))
+
+    def norm():
+        m = torch.nn.RMSNorm(d, eps=1e-6, device=dev, dtype=torch.bfloat16)
+        with torch.no_grad():
+            m.weight.copy_((1 + 0.1 * torch.randn(d, generator=g)).to(torch.bfloat16))
+        return m
+
+    layers = [MLPLayer(norm(), QuantizedMLP(lin(h, d), lin(h, d), lin(d, h))) for _ in range(n_layers)]
+    final = norm()
+    out = {}
+    for rows in rows_list:
+        hs = (torch.randn(rows, d, generator=g)).to(torch.bfloat16).to(dev)
+        rs = [(0.5 * torch.randn(rows, d, generator=g)).to(torch.bfloat16).to(dev) for _ in layers]
+        for _ in range(3):
+            stack_tail(hs, rs, layers, final)
+        torch.cuda.synchronize()
+        a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        a.record()
+        for _ in range(samples):
+            stack_tail(hs, rs, layers, final)
+        b.record()
+        torch.cuda.synchronize()
+        eager = a.elapsed_time(b) * 1e-3 / samples
+        gt = GraphedTail(layers, final, rows, d, dev)
+        gt(hs, rs)
+        torch.cuda.synchronize()
+        a.record()
+        for _ in range(samples):
+            gt.graph.replay()
+        b.record()
+        torch.cuda.synchronize()
+        graphed = a.elapsed_time(b) * 1e-3 / samples
+        out[f"rows={rows}"] = {"layers": n_layers, "eager_us": round(eager * 1e6, 1),
+                               "graph_us": round(graphed * 1e6, 1), "kernels_per_layer": 4}
+        log(f"[bench]   layer tail x{n_layers}, {rows} rows: eager {eager * 1e6:8.1f} us  graph {graphed * 1e6:8.1f} us")
+        del gt
+    return out
+
+
 def time_launches(torch, wl: Workload, m: int, samples: int) -> list[float]:
     """Per-launch kernel time (s) from HIP event pairs on the launch stream."""
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
@@ -301,6 +354,8 @@ def main() -> int:
     wl, res = head
     log("[bench] fused ops either side of the projection")
     fused = measure_fused(torch, lib, dev, wl)
+    log("[bench] verify-forward layer tails (MLP half), eager and graph-captured")
+    fused["layer_tail"] = measure_layer_tail(torch, dev)
     # Timed region: exactly K steps, synchronized on both sides.
     for _ in range(args.warmup):
         wl.step()

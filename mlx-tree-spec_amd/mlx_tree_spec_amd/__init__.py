@@ -9,9 +9,11 @@ this package does not load it, the first call does, and fails loudly if it is no
 from .fused_ops import add_rms_norm, add_rms_norm_
 from .packed_linear import STATS, QuantizedLinear, QuantizedMLP, eligible, install
 from .qmm import dequantize, gate_up_silu, pack_nax, quantized_matmul, unpack_nax
+from .verify import GraphedTail, MLPLayer, layer_tail, stack_tail
 
 __all__ = [
     "quantized_matmul", "gate_up_silu", "dequantize", "pack_nax", "unpack_nax", "add_rms_norm",
     "add_rms_norm_", "QuantizedLinear", "QuantizedMLP", "eligible", "install", "STATS",
+    "MLPLayer", "layer_tail", "stack_tail", "GraphedTail",
 ]
 __version__ = "0.1.0"

@@ -1,0 +1,110 @@
+"""The quantized layers of a batched verify forward, eager and captured in a HIP graph (needs an
+MI355X).
+
+Bars: the two-layer stack against the oracle's composition (fp32-accumulated projections, the
+oracle's norm and SiLU·mul, bf16 between ops) to the north-star tolerances (ulp-level differences
+of intermediate roundings propagate through the residual stream, so the whole chain is held to the
+tolerance rather than to bits); graph replays bit-equal to eager calls on the same inputs.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from mlx_tree_spec_amd import GraphedTail, MLPLayer, QuantizedLinear, QuantizedMLP, stack_tail
+from oracle import cpu
+from oracle import qmm4_oracle as O
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda:0"
+D, H, EPS = 512, 1024, 1e-6
+
+
+def bf16_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint16).view(np.int16)).view(torch.bfloat16).to(DEV)
+
+
+def u32_dev(a):
+    return torch.from_numpy(np.ascontiguousarray(a, dtype=np.uint32).view(np.int32)).to(DEV)
+
+
+def host_bits(t):
+    return t.view(torch.int16).cpu().numpy().view(np.uint16)
+
+
+def make_stack(n_layers=2, seed=0):
+    rng = np.random.default_rng(seed)
+    layers, ref = [], []
+
+    def lin(n, k, s):
+        _, w, sc, b = O.make_inputs(1, k, n, seed=s)
+        return QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(sc), bf16_dev(b)), (w, sc, b)
+
+    def norm():
+        wn = O.f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
+        m = torch.nn.RMSNorm(D, eps=EPS, device=DEV, dtype=torch.bfloat16)
+        with torch.no_grad():
+            m.weight.copy_(bf16_dev(wn))
+        return m, wn
+
+    for i in range(n_layers):
+        post, wpost = norm()
+        g, gw = lin(H, D, 100 * seed + 10 * i + 1)
+        u, uw = lin(H, D, 100 * seed + 10 * i + 2)
+        d, dw = lin(D, H, 100 * seed + 10 * i + 3)
+        layers.append(MLPLayer(post, QuantizedMLP(g, u, d)))
+        gu = tuple(np.concatenate([a, c]) for a, c in zip(gw, uw))
+        ref.append((wpost, gu, dw))
+    final, wfinal = norm()
+    return layers, final, ref, wfinal
+
+
+def oracle_stack(h, rs, ref, wfinal):
+    """The same layers on the CPU: oracle norm, fp32-accumulated projections rounded to bf16."""
+    x = None
+    for i, (wpost, gu, dw) in enumerate(ref):
+        h, x = O.add_rms_norm(h, rs[i], wpost, EPS)
+        t = O.f32_to_bf16_bits(cpu.qmm_f32(x, *gu))
+        a = O.silu_mul(t[:, :H], t[:, H:])
+        mo = O.f32_to_bf16_bits(cpu.qmm_f32(a, *dw))
+        wn = ref[i + 1][0] if i + 1 < len(ref) else wfinal
+        h, x = O.add_rms_norm(h, mo, wn, EPS)
+    return h, x
+
+
+def inputs(rows, n_layers, seed):
+    rng = np.random.default_rng(seed)
+    h = O.f32_to_bf16_bits(rng.standard_normal((rows, D)).astype(np.float32))
+    rs = [O.f32_to_bf16_bits((0.5 * rng.standard_normal((rows, D))).astype(np.float32)) for _ in range(n_layers)]
+    return h, rs
+
+
+# M = the sum of the requests' tree nodes: one decode request of 3 nodes (row-split kernels), and
+# 4 requests x 16 nodes (verify kernels, two-pass gate+up).
+@pytest.mark.parametrize("rows", [3, 64])
+def test_stack_tail_matches_oracle_composition(rows):
+    layers, final, ref, wfinal = make_stack()
+    h, rs = inputs(rows, len(layers), rows)
+    hg, xg = stack_tail(bf16_dev(h), [bf16_dev(r) for r in rs], layers, final)
+    ho, xo = oracle_stack(h, rs, ref, wfinal)
+    for got, want in ((hg, ho), (xg, xo)):
+        g = O.bf16_bits_to_f32(host_bits(got)).astype(np.float64)
+        w = O.bf16_bits_to_f32(want).astype(np.float64)
+        print(f"  stack rows={rows}: max_rel={O.max_rel(g, w):.2e} mean_rel={O.mean_rel(g, w):.2e}", flush=True)
+        assert O.max_rel(g, w) <= O.MAX_REL_TOL and O.mean_rel(g, w) <= O.MEAN_REL_TOL
+
+
+@pytest.mark.parametrize("rows", [4, 64])
+def test_graphed_tail_replays_equal_eager(rows):
+    layers, final, _, _ = make_stack(seed=1)
+    gt = GraphedTail(layers, final, rows, D, DEV)
+    for rep in range(3):
+        h, rs = inputs(rows, len(layers), 1000 * rows + rep)
+        hd, rsd = bf16_dev(h), [bf16_dev(r) for r in rs]
+        he, xe = stack_tail(hd, rsd, layers, final)  # eager work between the replays
+        he, xe = host_bits(he), host_bits(xe)
+        torch.cuda.synchronize()
+        hr, xr = gt(hd, rsd)
+        torch.cuda.synchronize()
+        assert np.array_equal(host_bits(hr), he), f"replay {rep}: h differs from eager"
+        assert np.array_equal(host_bits(xr), xe), f"replay {rep}: x differs from eager"
