@@ -206,7 +206,13 @@ int qmm4_gate_up_silu_bf16(const void* x, const uint32_t* w, const void* scales,
   // Decode rows: the row-split kernel with the epilogue fused (one launch, no [M, N] round trip).
   qmm4::RowSplitPlan rplan;
   if (qmm4::rowsplit_plan((int)M, (int)N, (int)K, di->cus, true, &rplan)) {
-    e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
+    uint32_t* cnt = nullptr;
+    float* part = nullptr;
+    if (rplan.KS > 1) {
+      rc = get_workspace(dev, stream, (size_t)rplan.ranges * sizeof(uint32_t), rplan.part_bytes, &cnt, &part);
+      if (rc) return rc;
+    }
+    e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, part, cnt, (int)M, (int)N, (int)K, stream);
     if (e != hipSuccess) return hip_fail(e, "fused gate+up row-split kernel launch");
     return QMM4_OK;
   }
@@ -274,10 +280,17 @@ int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, cons
   }
 
 #ifndef QMM4_NO_ROWSPLIT
-  // Up to 4 rows and enough output columns to give every CU its own rows: the row-split kernel.
+  // Up to 4 rows and enough output columns to give every CU its own rows (whole K, or K in 2 or 4
+  // slices when N is small): the row-split kernel.
   qmm4::RowSplitPlan rplan;
   if (qmm4::rowsplit_plan((int)M, (int)N, (int)K, di->cus, false, &rplan)) {
-    e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, (int)M, (int)N, (int)K, stream);
+    uint32_t* rcnt = nullptr;
+    float* rpart = nullptr;
+    if (rplan.KS > 1) {
+      rc = get_workspace(dev, stream, (size_t)rplan.ranges * sizeof(uint32_t), rplan.part_bytes, &rcnt, &rpart);
+      if (rc) return rc;
+    }
+    e = qmm4::launch_rowsplit(rplan, xb, w, sb, bb, yb, rpart, rcnt, (int)M, (int)N, (int)K, stream);
     if (e != hipSuccess) return hip_fail(e, "row-split kernel launch");
     return QMM4_OK;
   }
@@ -295,9 +308,13 @@ int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, cons
   // The row-phase kernel stages scale rows with 16-byte loads. It serves more than 16 rows, and
   // up to 16 rows when N gives every wave its own blocks; fewer rows over a small N go to the
   // verify kernel (its stream-K ranges balance better when there is little work per CU).
+#ifndef QMM4_ROWPHASE_NARROW_MIN_M
+#define QMM4_ROWPHASE_NARROW_MIN_M 17
+#endif
   if (M >= QMM4_ROWPHASE_MIN_M && aligned(scales, 16) && aligned(biases, 16) && K % 512 == 0) {
     qmm4::RowPhasePlan pplan;
-    if (qmm4::rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) && (M > 16 || pplan.wide)) {
+    if (qmm4::rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) &&
+        (M >= QMM4_ROWPHASE_NARROW_MIN_M || pplan.wide)) {
       uint32_t* pcnt = nullptr;
       float* ppart = nullptr;
       if (pplan.S > 1) {

@@ -82,15 +82,21 @@ struct RowSplitPlan {
   int Nout;     // output columns (N, or N / 2 when fused)
   int R;        // output columns per workgroup
   int RB;       // 16-row blocks per workgroup: ceil(R / 16), or ceil(2R / 16) when fused
-  int SU;       // units per block (K / (128 V))
-  int blocks;   // workgroups
+  int SU;       // units per block (Kp / (128 V))
+  int KS;       // K slices per column range (1: whole K per workgroup)
+  int Kp;       // K per slice
+  int ranges;   // column ranges
+  int blocks;   // workgroups (ranges x KS)
+  size_t part_bytes;  // KS > 1: fp32 row sums in the workspace (counters: one per range)
   size_t smem;  // dynamic LDS bytes
 };
 // Fills `plan` and returns true when the shape suits the row-split kernel on `cus` CUs. N is the
 // number of weight rows (for the fused gate+up, both halves).
 bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan);
+// part / cnt: the workspace (plan.part_bytes, plan.ranges counters at zero) when plan.KS > 1.
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                           const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream);
+                           const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
+                           hipStream_t stream);
 
 // y[m, j] = silu_mul_bf16(t[m, j], t[m, n + j]) for t bf16 [M, 2n] (the unfused gate+up epilogue).
 hipError_t launch_silu_mul(const uint16_t* t, uint16_t* y, int M, int n, hipStream_t stream);

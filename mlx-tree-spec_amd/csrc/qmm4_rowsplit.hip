@@ -34,6 +34,7 @@
 //    and cut into 16-row blocks (one block may hold both). Each column's gate and up sums are
 //    formed exactly as above, rounded to bf16 (the values the unfused projection would store), and
 //    combined by silu_mul_bf16.
+#include <algorithm>
 #include <type_traits>
 
 #include "qmm4_common.h"
@@ -59,8 +60,14 @@ struct RowSplitParams {
   int Nout;  // output columns: N, or N / 2 for the fused gate+up
   int R;     // output columns per workgroup (a multiple of 4)
   int RB;    // 16-row blocks per workgroup: ceil(R / 16), or ceil(2R / 16) for the fused gate+up
-  int SU;    // units per block, K / (128 V)
+  int SU;    // units per block, Kp / (128 V)
+  int KS;    // K slices per column range (1: each workgroup all of K)
+  int Kp;    // K per slice
+  float* part;    // KS > 1: fp32 row sums [workgroup][row] (f32x4 over the rows of x)
+  uint32_t* cnt;  // KS > 1: arrivals per column range (0 between launches)
 };
+
+constexpr int kCoherent = 16;  // buffer access flag: bypass non-coherent caches (cross-CU partials)
 
 template <int V>
 struct Scales {
@@ -87,16 +94,17 @@ __device__ __forceinline__ Scales<V> load_scales(__amdgpu_buffer_rsrc_t r, uint3
 __host__ __device__ inline size_t rowsplit_xs_bytes(int K) { return (size_t)(K >> 7) * 16 * kRsMP * 16; }
 __host__ __device__ inline size_t rowsplit_part_bytes(int units) { return (size_t)units * 16 * 16; }
 
-template <int V, bool FUSED>
+// KSPLIT: K in P.KS slices (false: whole K, the slice arithmetic and the merge compiled out).
+template <int V, bool FUSED, bool KSPLIT>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  const int S = P.K >> 7;  // super-steps per row
+  const int S = P.Kp >> 7;  // super-steps per row in this workgroup's K slice
   const int SU = P.SU;
   const int U = P.RB * SU;
   u32x4* xs = reinterpret_cast<u32x4*>(lds);
-  f32x4* part = reinterpret_cast<f32x4*>(lds + rowsplit_xs_bytes(P.K));
-  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.K) + rowsplit_part_bytes(U));
+  f32x4* part = reinterpret_cast<f32x4*>(lds + rowsplit_xs_bytes(P.Kp));
+  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.Kp) + rowsplit_part_bytes(U));
   int* next = reinterpret_cast<int*>(spare + 1);
 
   const int tid = threadIdx.x;
@@ -104,7 +112,10 @@ void rowsplit_kernel(RowSplitParams P) {
   // then live in scalar registers and buffer resources need no per-lane loop).
   const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int r0 = blockIdx.x * P.R;
+  // Column range and K slice of this workgroup.
+  const int range = KSPLIT ? blockIdx.x / P.KS : blockIdx.x;
+  const int kq = KSPLIT ? (blockIdx.x - range * P.KS) * P.Kp : 0;
+  const int r0 = range * P.R;
   const int r1 = min(P.Nout, r0 + P.R);
   const int KG = P.K >> 6;
 
@@ -124,7 +135,8 @@ void rowsplit_kernel(RowSplitParams P) {
     for (int j = 0; j < kRsXB; ++j) {
       const int i = tid + (batch * kRsXB + j) * kRsThreads;
       const int sq = i / P.M, m = i - sq * P.M;
-      const uint32_t off = i < xitems ? ((uint32_t)m * (uint32_t)P.K + (uint32_t)sq * 8u) * 2u : 0x80000000u;
+      const uint32_t off =
+          i < xitems ? ((uint32_t)m * (uint32_t)P.K + (uint32_t)kq + (uint32_t)sq * 8u) * 2u : 0x80000000u;
       xr[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
     }
   };
@@ -174,10 +186,13 @@ void rowsplit_kernel(RowSplitParams P) {
         const_cast<uint16_t*>(P.s), 0, live ? srec : 0, kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(P.b), 0, live ? srec : 0, kBufferRsrcWord3);
+    // The unit's byte offsets within the row: its K slice (kq / 2 code bytes, kq / 32 scale
+    // bytes) plus its step.
 #pragma unroll
-    for (int v = 0; v < V; ++v) wv[j][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + v * 64, st * V * 64, 0);
-    sv[j] = load_scales<V>(rs, so, st * 4 * V);
-    bv[j] = load_scales<V>(rb, so, st * 4 * V);
+    for (int v = 0; v < V; ++v)
+      wv[j][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + v * 64, (kq >> 1) + st * V * 64, 0);
+    sv[j] = load_scales<V>(rs, so, (kq >> 5) + st * 4 * V);
+    bv[j] = load_scales<V>(rb, so, (kq >> 5) + st * 4 * V);
   };
   // The ring holds units in the order they were taken, so the first unit past the end ends it.
   int ua = wave, ub = wave + kRsWaves;
@@ -267,24 +282,55 @@ void rowsplit_kernel(RowSplitParams P) {
     }
     return sum;
   };
+  auto write = [&](int col, const f32x4& sum, const f32x4& sup) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < kRsMP; ++m)
+      if (m < P.M) {
+        const uint32_t o = FUSED ? silu_mul_bf16(bf16_rne(sum[m]), bf16_rne(sup[m])) : bf16_rne(sum[m]);
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)o, ry, (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
+      }
+  };
+  if constexpr (!KSPLIT) {
+    for (int c = tid; c < P.R; c += kRsThreads) {
+      const int col = r0 + c;
+      if (col >= r1) continue;
+      write(col, row_sum(c), FUSED ? row_sum(P.R + c) : f32x4{});
+    }
+    return;
+  }
+
+  // K slices: store this workgroup's fp32 row sums, count in, and let the last workgroup of the
+  // column range add the slices in slice order (the same bits whichever arrives last).
+  const int RR = FUSED ? 2 * P.R : P.R;
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      P.part, 0, rsrc_bytes((unsigned long long)gridDim.x * RR * 16), kBufferRsrcWord3);
+  for (int lrow = tid; lrow < RR; lrow += kRsThreads)
+    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, row_sum(lrow)), rp,
+                                           ((uint32_t)blockIdx.x * RR + lrow) * 16u, 0, kCoherent);
+  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  __syncthreads();
+  if (tid == 0) {
+    const uint32_t prev = __hip_atomic_fetch_add(&P.cnt[range], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    *next = prev == (uint32_t)(P.KS - 1) ? 1 : 0;
+  }
+  __syncthreads();
+  if (*next == 0) return;
+  auto slice_sum = [&](int lrow) __attribute__((always_inline)) {
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int qq = 0; qq < P.KS; ++qq) {
+      const f32x4 c = __builtin_bit_cast(
+          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((uint32_t)(range * P.KS + qq) * RR + lrow) * 16u, 0,
+                                                       kCoherent));
+      sum[0] += c[0]; sum[1] += c[1]; sum[2] += c[2]; sum[3] += c[3];
+    }
+    return sum;
+  };
   for (int c = tid; c < P.R; c += kRsThreads) {
     const int col = r0 + c;
     if (col >= r1) continue;
-    const f32x4 sum = row_sum(c);
-    if constexpr (FUSED) {
-      const f32x4 sup = row_sum(P.R + c);
-#pragma unroll
-      for (int m = 0; m < kRsMP; ++m)
-        if (m < P.M)
-          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)silu_mul_bf16(bf16_rne(sum[m]), bf16_rne(sup[m])), ry,
-                                                (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
-    } else {
-#pragma unroll
-      for (int m = 0; m < kRsMP; ++m)
-        if (m < P.M)
-          __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_rne(sum[m]), ry, (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
-    }
+    write(col, slice_sum(c), FUSED ? slice_sum(P.R + c) : f32x4{});
   }
+  if (tid == 0) __hip_atomic_store(&P.cnt[range], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -292,54 +338,75 @@ void rowsplit_kernel(RowSplitParams P) {
 bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan) {
   if (M < 1 || M > kRsMP || cus < 1) return false;
   if (fused && N % 32 != 0) return false;
-  const int S = K >> 7;
-  // Units of 4 super-steps (256 bytes of a row: two whole 128-byte lines) where K allows: a unit
-  // boundary inside a line splits it between two waves' fetches.
-  const int V = S % 4 == 0 ? 4 : S % 5 == 0 ? 5 : 0;
-  if (V == 0) return false;
-  const int nout = fused ? N / 2 : N;
-  const int R = ((nout + cus - 1) / cus + 3) / 4 * 4;
-  const int RB = ((fused ? 2 * R : R) + 15) / 16;
-  const int SU = S / V;
-  // At least 4 blocks per workgroup (the decomposition only pays when rows alone fill the GPU).
-  if (RB < 4) return false;
-  const size_t smem = rowsplit_xs_bytes(K) + rowsplit_part_bytes(RB * SU) + 32;
-  if (smem > 160 * 1024) return false;
   // Row offsets of this kernel stay below 1 GiB.
   if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 30)) return false;
-  plan->V = V;
-  plan->fused = fused;
-  plan->Nout = nout;
-  plan->R = R;
-  plan->RB = RB;
-  plan->SU = SU;
-  plan->blocks = (nout + R - 1) / R;
-  plan->smem = smem;
-  return true;
+  const int nout = fused ? N / 2 : N;
+  // Whole K per workgroup when the columns alone give every CU at least 4 row blocks; otherwise
+  // K in 2 or 4 slices over as many workgroups per column range, when each workgroup still has
+  // at least 3 units per wave.
+  for (int ks = 1; ks <= 4; ks *= 2) {
+    if (K % (128 * ks) != 0) continue;
+    const int kp = K / ks;
+    const int S = kp >> 7;
+    // Units of 4 super-steps (256 bytes of a row: two whole 128-byte lines) where K allows: a unit
+    // boundary inside a line splits it between two waves' fetches.
+    const int V = S % 4 == 0 ? 4 : S % 5 == 0 ? 5 : 0;
+    if (V == 0) continue;
+    const int target = std::max(1, cus / ks);
+    const int R = ((nout + target - 1) / target + 3) / 4 * 4;
+    const int RB = ((fused ? 2 * R : R) + 15) / 16;
+    const int SU = S / V;
+    if (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves) continue;
+    const size_t smem = rowsplit_xs_bytes(kp) + rowsplit_part_bytes(RB * SU) + 32;
+    if (smem > 160 * 1024) continue;
+    const int ranges = (nout + R - 1) / R;
+    plan->V = V;
+    plan->fused = fused;
+    plan->Nout = nout;
+    plan->R = R;
+    plan->RB = RB;
+    plan->SU = SU;
+    plan->KS = ks;
+    plan->Kp = kp;
+    plan->ranges = ranges;
+    plan->blocks = ranges * ks;
+    plan->part_bytes = ks > 1 ? (size_t)plan->blocks * (fused ? 2 * R : R) * 16 : 0;
+    plan->smem = smem;
+    return true;
+  }
+  return false;
 }
 
-template <int V, bool FUSED>
+template <int V, bool FUSED, bool KSPLIT>
 hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rowsplit_kernel<V, FUSED>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rowsplit_kernel<V, FUSED, KSPLIT>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((rowsplit_kernel<V, FUSED>), dim3(plan.blocks), dim3(kRsThreads), plan.smem, stream, P);
+  hipLaunchKernelGGL((rowsplit_kernel<V, FUSED, KSPLIT>), dim3(plan.blocks), dim3(kRsThreads), plan.smem, stream, P);
   return hipGetLastError();
 }
 
+template <int V, bool FUSED>
+hipError_t launch_rowsplit_k(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
+  return plan.KS > 1 ? launch_rowsplit_t<V, FUSED, true>(plan, P, stream)
+                     : launch_rowsplit_t<V, FUSED, false>(plan, P, stream);
+}
+
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                           const uint16_t* b, uint16_t* y, int M, int N, int K, hipStream_t stream) {
+                           const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
+                           hipStream_t stream) {
   RowSplitParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
   P.Nout = plan.Nout; P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
+  P.KS = plan.KS; P.Kp = plan.Kp; P.part = part; P.cnt = cnt;
   if (plan.fused)
-    return plan.V == 5 ? launch_rowsplit_t<5, true>(plan, P, stream) : launch_rowsplit_t<4, true>(plan, P, stream);
-  return plan.V == 5 ? launch_rowsplit_t<5, false>(plan, P, stream) : launch_rowsplit_t<4, false>(plan, P, stream);
+    return plan.V == 5 ? launch_rowsplit_k<5, true>(plan, P, stream) : launch_rowsplit_k<4, true>(plan, P, stream);
+  return plan.V == 5 ? launch_rowsplit_k<5, false>(plan, P, stream) : launch_rowsplit_k<4, false>(plan, P, stream);
 }
 
 }  // namespace qmm4

@@ -265,6 +265,44 @@ def test_rowsplit_shapes(m, k, n):
     check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"row-split {m}x{k}x{n}", (x, w, s, b))
 
 
+# Up to 4 rows over an N too small for every CU to own 4 row blocks over all of K: K in 2 or 4
+# slices per column range, the last workgroup of a range adding the slices' fp32 sums in slice
+# order. 5120 x 17408 is the decode down projection; N = 5168 leaves a partial last range; K =
+# 34816 with N = 4096 gives slices of 17408.
+@pytest.mark.parametrize("m,k,n", [(1, 17408, 5120), (4, 17408, 5120), (2, 17408, 5168), (3, 34816, 4096)])
+def test_rowsplit_k_slices(m, k, n):
+    note(f"row-split K slices {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=m * 13 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split K slices {m}x{k}x{n}", (x, w, s, b))
+    # deterministic whichever slice arrives last; the arrival counters are back at zero
+    for _ in range(3):
+        assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
+def test_rowsplit_k_slices_one_hot_is_exact_dequant():
+    """One-hot rows in the first and the second K slice: each output is one dequantized weight."""
+    n, k, m = 5120, 17408, 4
+    rng = np.random.default_rng(21)
+    s, b = scale_bias_pairs("mixed", n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in (0, 8700, 8704, k - m):
+        ks = k0 + np.arange(m)
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), ks] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.empty((m, n), dtype=np.uint16)
+        for i, kk in enumerate(ks):
+            g = kk // 64
+            ref[i] = O.dequantize(w[:, 8 * g:8 * g + 8], s[:, g:g + 1], b[:, g:g + 1])[:, kk - 64 * g]
+        keep = (ref & 0x7F80) != 0
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}"
+
+
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 def test_rowsplit_one_hot_is_exact_dequant(kind):
     """One-hot rows of x on the row-split path: each output is one dequantized weight and must
