@@ -24,6 +24,11 @@
 //  * The next phase's x slice (A-fragment order) and the scales and biases of the range's rows are
 //    staged in LDS (double-buffered) by the whole workgroup, behind the weight prefetch; one
 //    barrier per phase publishes them.
+//  * Nothing waits for a load before it is needed: the phase barrier is a bare s_barrier behind
+//    an explicit count (a __syncthreads() fence would wait for the DMA of the phases ahead), the
+//    weight refills are issued outside any branch (a load issued in both arms of a branch leaves
+//    register copies at the join, and each copy waits for every older load), and the next scale
+//    window is loaded into registers one phase before its first use where registers allow.
 //  * The result leaves through LDS as 16-byte row chunks of y (or as fp32 partial tiles).
 #include <type_traits>
 
@@ -89,6 +94,7 @@ void rowphase_kernel(RowPhaseParams P) {
   constexpr int kRpWaves = C::kRpWaves, kRpThreads = C::kRpThreads;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   __shared__ int s_last;
+  __shared__ int s_bad[2];  // per window parity: a scale outside the fast range
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -147,34 +153,39 @@ void rowphase_kernel(RowPhaseParams P) {
 
   // ---- scale window: groups of phases [ph0, ph0 + WP) of the range's rows, 16-byte pieces of
   // each row's contiguous run (every scale line is read once per window, not once per phase).
-  // Returns whether this thread saw a scale outside the fast dequantization's range. Blocking:
-  // the caller has made sure that no wave still reads the previous window. ----
-  auto stage_window = [&](int ph0) __attribute__((always_inline)) {
-    constexpr int kPR = C::kWB / 16;  // pieces per row
-    const int g0 = ph0 * (2 * V);     // first group of the window
-    bool bad = false;
-    // Scales, then biases (one array's pieces in registers at a time).
+  // Loaded into registers (scales, then biases), then stored to LDS once no wave still reads the
+  // previous window. ----
+  constexpr int kPR = C::kWB / 16;  // window pieces per row
+  auto load_window = [&](int ph0, u32x4 (&r)[2][C::kWL]) __attribute__((always_inline)) {
+    const int g0 = ph0 * (2 * V);  // first group of the window
 #pragma unroll
-    for (int arr = 0; arr < 2; ++arr) {
-      u32x4 r[C::kWL];
+    for (int arr = 0; arr < 2; ++arr)
 #pragma unroll
       for (int j = 0; j < C::kWL; ++j) {
         const int i = tid + j * kRpThreads;
         const int row = i / kPR, pc = i - row * kPR;
         const bool ok = row < nrows && g0 + pc * 8 < KG;
         const uint32_t off = ok ? (uint32_t)(r0 + row) * (uint32_t)KG * 2u + (uint32_t)(g0 + pc * 8) * 2u : kOut;
-        r[j] = __builtin_amdgcn_raw_buffer_load_b128(arr == 0 ? rs : rb, off, 0, 0);
+        r[arr][j] = __builtin_amdgcn_raw_buffer_load_b128(arr == 0 ? rs : rb, off, 0, 0);
       }
+  };
+  // Returns whether this thread saw a scale outside the fast dequantization's range.
+  auto store_window = [&](const u32x4 (&r)[2][C::kWL]) __attribute__((always_inline)) {
+    bool bad = false;
+#pragma unroll
+    for (int arr = 0; arr < 2; ++arr) {
       u32x4* d = reinterpret_cast<u32x4*>(arr == 0 ? ws_s : ws_b);
 #pragma unroll
       for (int j = 0; j < C::kWL; ++j) {
         const int i = tid + j * kRpThreads;
-        if (i < RW * kPR) {
+        // (Every variant's window is a whole number of pieces per thread: no store is skipped, so
+        // no load is left pending on one path of a branch.)
+        if ((RW * kPR) % kRpThreads == 0 || i < RW * kPR) {
           const int row = i / kPR, pc = i - row * kPR;
-          d[row * (C::kWS / 16) + pc] = r[j];
+          d[row * (C::kWS / 16) + pc] = r[arr][j];
           if (arr == 0) {
 #pragma unroll
-            for (int e = 0; e < 4; ++e) bad |= !fast_scale_ok(r[j][e] & 0xFFFFu) || !fast_scale_ok(r[j][e] >> 16);
+            for (int e = 0; e < 4; ++e) bad |= !fast_scale_ok(r[arr][j][e] & 0xFFFFu) || !fast_scale_ok(r[arr][j][e] >> 16);
           }
         }
       }
@@ -206,48 +217,58 @@ void rowphase_kernel(RowPhaseParams P) {
 #pragma unroll
     for (int i = 0; i < MB; ++i) acc[j][i] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // ---- one phase: LDS stage `st`, register buffer J; piece v of every block is refilled with
-  // phase `nph` (two phases ahead) as soon as super-step v has been used ----
-  auto compute = [&](int st, int pw, auto jc, auto fast, int nph, bool nlive) __attribute__((always_inline)) {
+  // ---- super-step v of one phase: LDS stage `st`, register buffer J ----
+  auto compute_v = [&](int st, int pw, int v, auto jc, auto fast) __attribute__((always_inline)) {
     constexpr int J = decltype(jc)::value;
     constexpr bool FAST = decltype(fast)::value;
     const u32x4* xb = xs(st);
     // Phase pw of the window: dwords pw * V .. pw * V + V - 1 of each row's window run.
     const uint32_t* sb32 = reinterpret_cast<const uint32_t*>(ws_s) + pw * V;
     const uint32_t* bb32 = reinterpret_cast<const uint32_t*>(ws_b) + pw * V;
+    // This lane's words of super-step v lie in group 2 v + g / 2 of the phase; dword v of row
+    // (wave + W j) * 16 + n holds groups 2 v and 2 v + 1.
+    float c1[BPW], c2[BPW], bfv[BPW];
 #pragma unroll
-    for (int v = 0; v < V; ++v) {
-      // This lane's words of super-step v lie in group 2 v + g / 2 of the phase; dword v of row
-      // (wave + W j) * 16 + n holds groups 2 v and 2 v + 1.
-      float c1[BPW], c2[BPW], bfv[BPW];
+    for (int j = 0; j < BPW; ++j) {
+      const int lrow = 16 * (wave + kRpWaves * j) + n;
+      const uint32_t sd = sb32[lrow * (C::kWS / 4) + v];
+      const uint32_t bd = bb32[lrow * (C::kWS / 4) + v];
+      const uint32_t sbits = (g >> 1) ? (sd >> 16) : (sd & 0xFFFFu);
+      const uint32_t bbits = (g >> 1) ? (bd >> 16) : (bd & 0xFFFFu);
+      const float sf = bf16_to_f32(sbits);
+      bfv[j] = bf16_to_f32(bbits);
+      c1[j] = FAST ? sf * 16777216.0f : sf;
+      c2[j] = FAST ? sf * 1048576.0f : sf * 0.0625f;
+    }
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+      u32x4 a[MB];
+#pragma unroll
+      for (int i = 0; i < MB; ++i) a[i] = xb[(v * 16 + g * 4 + t) * MP + i * 16 + n];
+      // Blocks past this wave's count hold zero weights (their loads lie outside the buffer)
+      // and sums that are never stored: computing them keeps the loop free of branches.
 #pragma unroll
       for (int j = 0; j < BPW; ++j) {
-        const int lrow = 16 * (wave + kRpWaves * j) + n;
-        const uint32_t sd = sb32[lrow * (C::kWS / 4) + v];
-        const uint32_t bd = bb32[lrow * (C::kWS / 4) + v];
-        const uint32_t sbits = (g >> 1) ? (sd >> 16) : (sd & 0xFFFFu);
-        const uint32_t bbits = (g >> 1) ? (bd >> 16) : (bd & 0xFFFFu);
-        const float sf = bf16_to_f32(sbits);
-        bfv[j] = bf16_to_f32(bbits);
-        c1[j] = FAST ? sf * 16777216.0f : sf;
-        c2[j] = FAST ? sf * 1048576.0f : sf * 0.0625f;
+        const u32x4 B = FAST ? dequant_word_fast(wv[J][j][v][t], c1[j], c2[j], bfv[j])
+                             : dequant_word(wv[J][j][v][t], c1[j], c2[j], bfv[j]);
+#pragma unroll
+        for (int i = 0; i < MB; ++i)
+          acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(B), acc[j][i], 0, 0, 0);
       }
+    }
+  };
+  // ---- one phase; piece v of every block is refilled with phase `nph` (two phases ahead) as
+  // soon as super-step v has been used. The refills stay outside the branch on the
+  // dequantization form: loads issued in both arms of a branch leave register copies at the
+  // join, and a copy of a register still being loaded waits for every load issued before it. ----
+  auto compute = [&](int st, int pw, auto jc, bool fast, int nph, bool nlive) __attribute__((always_inline)) {
+    constexpr int J = decltype(jc)::value;
 #pragma unroll
-      for (int t = 0; t < 4; ++t) {
-        u32x4 a[MB];
-#pragma unroll
-        for (int i = 0; i < MB; ++i) a[i] = xb[(v * 16 + g * 4 + t) * MP + i * 16 + n];
-        // Blocks past this wave's count hold zero weights (their loads lie outside the buffer)
-        // and sums that are never stored: computing them keeps the loop free of branches.
-#pragma unroll
-        for (int j = 0; j < BPW; ++j) {
-          const u32x4 B = FAST ? dequant_word_fast(wv[J][j][v][t], c1[j], c2[j], bfv[j])
-                               : dequant_word(wv[J][j][v][t], c1[j], c2[j], bfv[j]);
-#pragma unroll
-          for (int i = 0; i < MB; ++i)
-            acc[j][i] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(a[i]), as_bf16x8(B), acc[j][i], 0, 0, 0);
-        }
-      }
+    for (int v = 0; v < V; ++v) {
+      if (fast)
+        compute_v(st, pw, v, jc, std::true_type{});
+      else
+        compute_v(st, pw, v, jc, std::false_type{});
       fetch_v(J, v, nph, nlive);
     }
   };
@@ -262,7 +283,17 @@ void rowphase_kernel(RowPhaseParams P) {
   // Windows are aligned to absolute phases (WP-phase boundaries of K), so every 16-byte piece of
   // a window is 16-byte aligned. The window's loads return after the x loads above (the vector
   // memory count is in order), so its stores also find both x stages written.
-  bool winbad = __syncthreads_or(stage_window(pa - pa % C::WP)) != 0;
+  // Later windows are loaded into registers one phase ahead where the registers allow
+  // (accumulators, two weight buffers and the window within 150 of the 256 VGPRs); otherwise a
+  // window is loaded and stored at its first phase.
+  constexpr bool kWinAhead = 4 * BPW * MB + 8 * BPW * V + 8 * C::kWL <= 150;
+  u32x4 wr[2][C::kWL];
+  load_window(pa - pa % C::WP, wr);
+  if (tid == 0) {
+    s_bad[0] = 0;
+    s_bad[1] = 0;
+  }
+  bool winbad = __syncthreads_or(store_window(wr)) != 0;
 
   // Loads issued after the x of phase ph + 1 by the end of phase ph: the rest of phase ph - 1's
   // weight refills, the x of phase ph + 2 and phase ph's refills.
@@ -276,16 +307,34 @@ void rowphase_kernel(RowPhaseParams P) {
   auto phase = [&](int ph, auto jc) __attribute__((always_inline)) {
     const int k = ph - pa;
     const int st = k % 3, st2 = (k + 2) % 3, pw = ph % C::WP;
-    if (pw == 0 && k > 0) winbad = __syncthreads_or(stage_window(ph)) != 0;
+    if (pw == 0 && k > 0) {
+      if constexpr (kWinAhead) {
+        // The window's registers were loaded during the previous phase, and every wave is past
+        // its last read of the old window (the previous phase's barrier).
+        const int wpar = (ph / C::WP) & 1;
+        if (store_window(wr)) s_bad[wpar] = 1;
+        if (tid == 0) s_bad[wpar ^ 1] = 0;  // last read one window ago
+        asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        __builtin_amdgcn_sched_barrier(0);
+        __builtin_amdgcn_s_barrier();
+        __builtin_amdgcn_sched_barrier(0);
+        winbad = s_bad[wpar] != 0;
+      } else {
+        load_window(ph, wr);
+        winbad = __syncthreads_or(store_window(wr)) != 0;
+      }
+    }
     const bool live2 = ph + 2 < pb;
+    if (kWinAhead && pw == C::WP - 1 && ph + 1 < pb) load_window(ph + 1, wr);
     stage_x(st2, ph + 2, live2);
-    if (!winbad)
-      compute(st, pw, jc, std::true_type{}, ph + 2, live2);
-    else
-      compute(st, pw, jc, std::false_type{}, ph + 2, live2);
-    // The x of phase ph + 1 (issued at the start of phase ph - 1) is in LDS; publish it.
+    compute(st, pw, jc, !winbad, ph + 2, live2);
+    // The x of phase ph + 1 (issued at the start of phase ph - 1) is in LDS; publish it. A bare
+    // barrier: __syncthreads() would also wait for the x and weight loads of the phases ahead
+    // (its fence covers the LDS writes of the DMA still in flight).
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter) : "memory");
-    __syncthreads();
+    __builtin_amdgcn_sched_barrier(0);
+    __builtin_amdgcn_s_barrier();
+    __builtin_amdgcn_sched_barrier(0);
   };
   int i = 0;
   for (; i + 2 <= np; i += 2) {
