@@ -318,10 +318,10 @@ int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, cons
       uint32_t* pcnt = nullptr;
       float* ppart = nullptr;
       if (pplan.S > 1) {
-        rc = get_workspace(dev, stream, (size_t)pplan.ranges * sizeof(uint32_t), pplan.part_bytes, &pcnt, &ppart);
+        rc = get_workspace(dev, stream, 0, pplan.part_bytes, &pcnt, &ppart);
         if (rc) return rc;
       }
-      e = qmm4::launch_rowphase(pplan, xb, w, sb, bb, yb, ppart, pcnt, (int)M, (int)N, (int)K, stream);
+      e = qmm4::launch_rowphase(pplan, xb, w, sb, bb, yb, ppart, (int)M, (int)N, (int)K, stream);
       if (e != hipSuccess) return hip_fail(e, "row-phase kernel launch");
       return QMM4_OK;
     }

@@ -70,10 +70,10 @@ struct RowPhasePlan {
   bool wide;          // every workgroup takes all of K (N fills the GPU)
 };
 bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan);
-// `part` holds plan.part_bytes, `cnt` plan.ranges zeroed uint32s (used when plan.S > 1).
+// `part` holds plan.part_bytes (used when plan.S > 1: the partial tiles, added by a second kernel
+// launched behind the first on the same stream).
 hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                           const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
-                           hipStream_t stream);
+                           const uint16_t* b, uint16_t* y, float* part, int M, int N, int K, hipStream_t stream);
 
 // Row-split decode kernel (up to 4 rows, output columns split evenly over one workgroup per CU).
 struct RowSplitPlan {

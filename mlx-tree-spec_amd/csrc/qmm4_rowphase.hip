@@ -9,9 +9,9 @@
 //
 //  * Workgroup p (8 waves, two per SIMD) owns a range of 16-row weight blocks and a range of
 //    phases (PH = 128 V values of k each); the phase ranges of one block range partition K. When
-//    N alone fills the GPU every workgroup takes all of K; otherwise K is split and the
-//    workgroups of a block range add their fp32 partial tiles (the last to finish adds them in
-//    workgroup order, so results are deterministic).
+//    N alone fills the GPU every workgroup takes all of K; otherwise K is split, each workgroup
+//    stores its fp32 partial tile, and a second kernel adds each range's tiles in workgroup order
+//    (deterministic), one item per thread over the whole GPU.
 //  * Wave w owns blocks w, w + 8, w + 16, ... of the range (at most BPW) and holds one whole phase
 //    of their weights in registers while the next phase's weights are in flight (double buffer).
 //    Lane (n = lane % 16, g = lane / 16) loads V 16-byte pieces of row n of each block, piece v at
@@ -47,7 +47,6 @@ struct RowPhaseParams {
   const uint32_t* w;
   uint16_t* y;
   float* part;    // [G][items] f32x4 partial tiles (K split only)
-  uint32_t* cnt;  // [ranges] arrival counters; zero before and after every launch
   int M, N, K;
   int NB;         // 16-row blocks of w (N / 16)
   int BW;         // blocks per range
@@ -93,7 +92,6 @@ void rowphase_kernel(RowPhaseParams P) {
   constexpr int MB = C::MB, MP = C::MP, V = C::V, BPW = C::BPW, RW = C::RW;
   constexpr int kRpWaves = C::kRpWaves, kRpThreads = C::kRpThreads;
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
-  __shared__ int s_last;
   __shared__ int s_bad[2];  // per window parity: a scale outside the fast range
 
   const int tid = threadIdx.x;
@@ -380,8 +378,8 @@ void rowphase_kernel(RowPhaseParams P) {
     return;
   }
 
-  // K split: store this workgroup's fp32 partial tile (item (wave, j, i) lane-major), count in,
-  // and let the last workgroup of the range add the partials in workgroup order.
+  // K split: store this workgroup's fp32 partial tile (item (wave, j, i) lane-major); the reduce
+  // kernel that follows on the stream adds a range's partials in workgroup order.
   const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
       P.part, 0, rsrc_bytes((unsigned long long)gridDim.x * C::kItems * 16), kBufferRsrcWord3);
 #pragma unroll
@@ -393,43 +391,58 @@ void rowphase_kernel(RowPhaseParams P) {
         __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, acc[j][ii]), rp,
                                                ((uint32_t)p * C::kItems + item) * 16u, 0, kCoherent);
     }
-  asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-  __syncthreads();
-  if (tid == 0) {
-    const uint32_t prev = __hip_atomic_fetch_add(&P.cnt[range], 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    s_last = prev == (uint32_t)(P.S - 1) ? 1 : 0;
+}
+
+// K split, second pass: y from the S partial tiles of each block range, added in workgroup order
+// from +0 (the order a single workgroup adding them would use), one f32x4 item per thread. The
+// sum of a range used to be formed by the range's last workgroup alone: 12 tiles of 64 KB read by
+// one CU took 6.5-7.6 us at the end of the batched-verify down projection; spread over the GPU
+// the same bytes take a few microseconds.
+constexpr int kRedThreads = 256;
+template <class C>
+__global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhaseParams P) {
+  constexpr int MB = C::MB, BPW = C::BPW, kRpWaves = C::kRpWaves;
+  const int ranges = (P.NB + P.BW - 1) / P.BW;
+  const int it = blockIdx.x * kRedThreads + threadIdx.x;
+  const int range = it / C::kItems;
+  if (range >= ranges) return;
+  // Item = ((wave * BPW + j) * MB + ii) * 64 + lane of the first pass.
+  const int item = it - range * C::kItems;
+  const int lane = item & 63, rest = item >> 6;
+  const int ii = rest % MB, wj = rest / MB;
+  const int j = wj % BPW, wave = wj / BPW;
+  const int blk = wave + kRpWaves * j;  // block within the range
+  const int b0 = range * P.BW;
+  if (blk >= min(P.BW, P.NB - b0)) return;  // no such block: the first pass stored nothing
+  const int n = lane & 15, g = lane >> 4;
+  const int col = (b0 + blk) * 16 + n;
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      P.part, 0, rsrc_bytes((unsigned long long)ranges * P.S * C::kItems * 16), kBufferRsrcWord3);
+  f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  const uint32_t base = (uint32_t)range * (uint32_t)P.S;
+  // Four contributors' loads in flight at a time; past the last they read zero (an offset outside
+  // the buffer), and adding +0 leaves a sum that is not -0 unchanged (a sum from +0 never is -0).
+  for (int q = 0; q < P.S; q += 4) {
+    f32x4 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const uint32_t off = q + u < P.S ? ((base + (uint32_t)(q + u)) * C::kItems + (uint32_t)item) * 16u : 0x80000000u;
+      v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kCoherent));
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      sum[0] += v[u][0]; sum[1] += v[u][1]; sum[2] += v[u][2]; sum[3] += v[u][3];
+    }
   }
-  __syncthreads();
-  if (!s_last) return;
-  // Sum the range's partials: each lane its own items, contributors in order, loads in batches.
-  f32x4 sum[BPW][MB];
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
 #pragma unroll
-  for (int j = 0; j < BPW; ++j)
-#pragma unroll
-    for (int ii = 0; ii < MB; ++ii) sum[j][ii] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-  const int q0 = range * P.S;
-  for (int q = 0; q < P.S; ++q) {
-    f32x4 v[BPW][MB];
-#pragma unroll
-    for (int j = 0; j < BPW; ++j)
-#pragma unroll
-      for (int ii = 0; ii < MB; ++ii) {
-        const uint32_t item = (uint32_t)(((wave * BPW + j) * MB + ii) * 64 + lane);
-        const uint32_t off = j < nbw ? ((uint32_t)(q0 + q) * C::kItems + item) * 16u : kOut;
-        v[j][ii] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kCoherent));
-      }
-#pragma unroll
-    for (int j = 0; j < BPW; ++j)
-#pragma unroll
-      for (int ii = 0; ii < MB; ++ii) {
-        sum[j][ii][0] += v[j][ii][0]; sum[j][ii][1] += v[j][ii][1];
-        sum[j][ii][2] += v[j][ii][2]; sum[j][ii][3] += v[j][ii][3];
-      }
+  for (int r = 0; r < 4; ++r) {
+    const int m = ii * 16 + 4 * g + r;
+    if (m < P.M)
+      __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16x2(sum[r], 0.0f) & 0xFFFFu), ry,
+                                            ((uint32_t)m * (uint32_t)P.N + (uint32_t)col) * 2u, 0, 0);
   }
-  tile_to_lds(sum);
-  __syncthreads();
-  write_y();
-  if (tid == 0) __hip_atomic_store(&P.cnt[range], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
@@ -534,21 +547,28 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
 }
 
 hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                           const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
-                           hipStream_t stream) {
+                           const uint16_t* b, uint16_t* y, float* part, int M, int N, int K, hipStream_t stream) {
   RowPhaseParams P;
-  P.x = x; P.s = s; P.b = b; P.w = w; P.y = y; P.part = part; P.cnt = cnt;
+  P.x = x; P.s = s; P.b = b; P.w = w; P.y = y; P.part = part;
   P.M = M; P.N = N; P.K = K;
   P.NB = N / 16; P.BW = plan.BW; P.S = plan.S; P.NP = plan.NP;
   const void* f = rowphase_func(plan.variant);
   if (!f) return hipErrorInvalidValue;
   hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)plan.lds);
   if (e != hipSuccess) return e;
+  // K split: the reduce kernel's grid has one thread per f32x4 item of every range's tile.
   switch (plan.variant) {
-#define QMM4_RPL(i, m, vv, bb, w)                                                                          \
-  case i:                                                                                                 \
-    hipLaunchKernelGGL(rowphase_kernel<RpCfg##i>, dim3(plan.blocks), dim3(RpCfg##i::kRpThreads), plan.lds, \
-                       stream, P);                                                                        \
+#define QMM4_RPL(i, m, vv, bb, w)                                                                            \
+  case i:                                                                                                   \
+    hipLaunchKernelGGL(rowphase_kernel<RpCfg##i>, dim3(plan.blocks), dim3(RpCfg##i::kRpThreads), plan.lds,   \
+                       stream, P);                                                                          \
+    if (plan.S > 1) {                                                                                       \
+      e = hipGetLastError();                                                                                \
+      if (e != hipSuccess) return e;                                                                        \
+      const long long items = (long long)plan.ranges * RpCfg##i::kItems;                                    \
+      hipLaunchKernelGGL(rowphase_reduce_kernel<RpCfg##i>, dim3((unsigned)((items + kRedThreads - 1) / kRedThreads)), \
+                         dim3(kRedThreads), 0, stream, P);                                                  \
+    }                                                                                                       \
     break;
     QMM4_ROWPHASE_VARIANTS(QMM4_RPL)
 #undef QMM4_RPL

@@ -367,6 +367,39 @@ def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
         assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
 
 
+# Scale windows of the row-phase kernel are 32 groups (2048 values of k) of every row. Odd windows
+# here hold scales that need the general form, even windows only fast-form scales, so a workgroup
+# whose phases cross windows switches form at each window: wide ranges of 10 and 12 phases over 3
+# and 2 windows (windows loaded a phase ahead), the K-split batched-verify shape (ranges of 5-6
+# phases, some across a window edge), and a wide 32-row shape whose variant stages each window at
+# its first phase (5 blocks per wave leave no registers for a window ahead).
+@pytest.mark.parametrize("m,k,n", [(8, 5120, 34848), (48, 3072, 33024), (64, 17408, 5120), (32, 5120, 65552)])
+def test_rowphase_window_form_switches(m, k, n):
+    note(f"row-phase window switches {m}x{k}x{n}")
+    rng = np.random.default_rng(m * 7 + k)
+    groups = k // 64
+    s, b = scale_bias_pairs("fast", n * groups, rng)
+    sl, bl = scale_bias_pairs("slow", n * groups, rng)
+    s, b, sl, bl = (a.reshape(n, groups) for a in (s, b, sl, bl))
+    odd = ((np.arange(groups) // 32) % 2 == 1)[None, :]
+    s, b = np.where(odd, sl, s), np.where(odd, bl, b)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for win in range((k + 2047) // 2048):
+        k0 = min(2048 * win + 1000, k - m)
+        ks = k0 + np.arange(m)
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), ks] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.empty((m, n), dtype=np.uint16)
+        for i, kk in enumerate(ks):
+            g = kk // 64
+            ref[i] = O.dequantize(w[:, 8 * g:8 * g + 8], s[:, g:g + 1], b[:, g:g + 1])[:, kk - 64 * g]
+        keep = (ref & 0x7F80) != 0  # subnormal bf16 weights test the MFMA, not the dequant
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches in window {win}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 # ----------------------------------------------------------------------------- host integration
 def test_side_stream_and_workspace_growth():
     cases = [O.make_inputs(16, 5120, 512, seed=1), O.make_inputs(64, 17408, 1024, seed=2), O.make_inputs(3, 256, 64, seed=3)]
