@@ -45,7 +45,8 @@ extern "C" {
  *   (M + 256) * N * 2 bytes below 2^32), x and w 16-byte aligned, scales and biases
  *   4-byte aligned, y 2-byte aligned. M == 0 or N == 0 is a no-op. Rows M <= 64 run one of the
  *   HBM-bound verify/decode kernels (row-split for M <= 4 over a large N or a long K, row-phase for more than
- *   16 rows or a large N, K-split verify or stream-K skinny otherwise), larger M the MFMA GEMM; the
+ *   16 rows, a large N, or fewer rows when its K split fills half the CUs, K-split verify or
+ *   stream-K skinny otherwise), larger M the MFMA GEMM; the
  *   choice is a fixed function of the shape and the scale/bias alignment. Results are deterministic
  *   (bit-identical across calls and streams).
  */

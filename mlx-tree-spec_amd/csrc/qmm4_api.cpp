@@ -306,15 +306,16 @@ int dispatch_qmm(int dev, DeviceInfo* di, const void* x, const uint32_t* w, cons
 #endif
 #ifndef QMM4_NO_ROWPHASE
   // The row-phase kernel stages scale rows with 16-byte loads. It serves more than 16 rows, and
-  // up to 16 rows when N gives every wave its own blocks; fewer rows over a small N go to the
-  // verify kernel (its stream-K ranges balance better when there is little work per CU).
+  // up to 16 rows when its plan fills at least half the CUs; fewer rows over a small N with K
+  // split too few ways go to the verify kernel (its stream-K ranges balance better when there is
+  // little work per CU).
 #ifndef QMM4_ROWPHASE_NARROW_MIN_M
 #define QMM4_ROWPHASE_NARROW_MIN_M 17
 #endif
   if (M >= QMM4_ROWPHASE_MIN_M && aligned(scales, 16) && aligned(biases, 16) && K % 512 == 0) {
     qmm4::RowPhasePlan pplan;
     if (qmm4::rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) &&
-        (M >= QMM4_ROWPHASE_NARROW_MIN_M || pplan.wide)) {
+        (pplan.wide || M >= QMM4_ROWPHASE_NARROW_MIN_M || 2 * pplan.blocks >= di->cus)) {
       uint32_t* pcnt = nullptr;
       float* ppart = nullptr;
       if (pplan.S > 1) {
