@@ -304,8 +304,8 @@ def main() -> int:
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
-        log("bench.py measures one GPU: this build has no multi-GPU path (the kernel is per-GPU; "
-            "sharding over output columns is described in DESIGN.md). Run with --gpus 1.")
+        log("bench.py measures one GPU: there is no multi-GPU path (the kernel is per-GPU; the "
+            "path would shard over output columns, which is not built). Run with --gpus 1.")
         return 2
 
     import torch

@@ -1,5 +1,6 @@
 """Test infrastructure: CPU oracle of the packed 4-bit affine quantized matmul.
 
 Importable only from tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg, where it is
-the checker (or the timed CPU baseline), never the thing measured or shipped.
+the reference results are checked against (or the timed CPU baseline), never the thing measured
+or shipped.
 """

@@ -1,4 +1,4 @@
-"""ctypes binding of oracle/qmm4_cpu.c — TEST INFRASTRUCTURE (checker and timed CPU baseline).
+"""ctypes binding of oracle/qmm4_cpu.c — TEST INFRASTRUCTURE (test reference and timed CPU baseline).
 
 Loads the AVX-512 build where the host CPU has AVX-512 F/BW/VL, else the AVX2 build. Both are
 built by `make -C oracle` (also run by __graft_entry__.build()).

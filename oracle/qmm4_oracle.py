@@ -1,7 +1,7 @@
 """CPU oracle for the packed 4-bit affine quantized matmul (MLX format) — TEST INFRASTRUCTURE.
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import this module, and
-only as the checker: the product path (mlx-tree-spec_amd/) never calls it and fails loudly when
+only as the reference results are checked against: the product path (mlx-tree-spec_amd/) never calls it and fails loudly when
 its HIP library is missing.
 
 Restates, in numpy, the reference's arithmetic for the path:

@@ -3,7 +3,7 @@
 Bars:
   * dequantize: bit-exact against the exact-rational brute-force table, and against the oracle
     over every finite bf16 scale and random model-sized weights;
-  * quantized_matmul: the north-star tolerance against the fp32-accumulated reference
+  * quantized_matmul: the parity tolerance against the fp32-accumulated reference
     (max|y-ref|/max|ref| <= 1e-2, mean|y-ref|/mean|ref| <= 2e-3), and, much tighter, per element:
     at least 99% of outputs equal bf16_rne(ref) and every other output is within one bf16 ulp of
     ref plus 2^-17 * sum_k |x||w| (only the fp32 accumulation order differs from the oracle);
@@ -58,7 +58,7 @@ def abs_dot(x, w, s, b, rows, cols):
 
 
 def check_qmm(y_bits, ref, what="", inputs=None):
-    """North-star tolerances, plus per element: at least 99% of outputs equal bf16_rne(ref), and
+    """max_rel <= 1e-2 and mean_rel <= 2e-3, plus per element: at least 99% of outputs equal bf16_rne(ref), and
     every other one is within one bf16 ulp of ref plus 2^-17 * sum_k |x||w| (fp32 accumulation
     in another order can move a result near zero by many of its own ulps, never by more)."""
     ref = np.asarray(ref, dtype=np.float64)

@@ -2,7 +2,7 @@
 MI355X).
 
 Bars: the two-layer stack against the oracle's composition (fp32-accumulated projections, the
-oracle's norm and SiLU·mul, bf16 between ops) to the north-star tolerances (ulp-level differences
+oracle's norm and SiLU·mul, bf16 between ops) to max_rel <= 1e-2 and mean_rel <= 2e-3 (ulp-level differences
 of intermediate roundings propagate through the residual stream, so the whole chain is held to the
 tolerance rather than to bits); graph replays bit-equal to eager calls on the same inputs.
 """
