@@ -1,7 +1,7 @@
 /*
  * CPU restatement of the packed 4-bit affine quantized matmul — TEST INFRASTRUCTURE.
  *
- * Used only as the checker in tests/ and as the timed CPU baseline ("port") in bench.py; the
+ * Used only as the test reference in tests/ and as the timed CPU baseline ("port") in bench.py; the
  * product path never links it. Same arithmetic as oracle/qmm4_oracle.py:
  *   q[n, 8c+i] = (w[n, c] >> 4i) & 0xF                     src/mlx_tree_spec/qmm_packed.py:115, 200-201
  *   w_deq     = bf16_rne(fp32(s) * q + fp32(b)), g = k/64  qmm_packed.py:635-636, 630
