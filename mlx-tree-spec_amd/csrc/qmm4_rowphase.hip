@@ -399,6 +399,9 @@ void rowphase_kernel(RowPhaseParams P) {
 // one CU took 6.5-7.6 us at the end of the batched-verify down projection; spread over the GPU
 // the same bytes take a few microseconds.
 constexpr int kRedThreads = 256;
+#ifndef QMM4_RP_REDUCE_BATCH
+#define QMM4_RP_REDUCE_BATCH 16
+#endif
 template <class C>
 __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhaseParams P) {
   constexpr int MB = C::MB, BPW = C::BPW, kRpWaves = C::kRpWaves;
@@ -420,17 +423,19 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
       P.part, 0, rsrc_bytes((unsigned long long)ranges * P.S * C::kItems * 16), kBufferRsrcWord3);
   f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t base = (uint32_t)range * (uint32_t)P.S;
-  // Four contributors' loads in flight at a time; past the last they read zero (an offset outside
-  // the buffer), and adding +0 leaves a sum that is not -0 unchanged (a sum from +0 never is -0).
-  for (int q = 0; q < P.S; q += 4) {
-    f32x4 v[4];
+  // kRedBatch contributors' loads in flight at a time (one memory round trip for the usual S of
+  // 10-12); past the last they read zero (an offset outside the buffer), and adding +0 leaves a
+  // sum that is not -0 unchanged (a sum from +0 never is -0).
+  constexpr int kRedBatch = QMM4_RP_REDUCE_BATCH;
+  for (int q = 0; q < P.S; q += kRedBatch) {
+    f32x4 v[kRedBatch];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kRedBatch; ++u) {
       const uint32_t off = q + u < P.S ? ((base + (uint32_t)(q + u)) * C::kItems + (uint32_t)item) * 16u : 0x80000000u;
       v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kCoherent));
     }
 #pragma unroll
-    for (int u = 0; u < 4; ++u) {
+    for (int u = 0; u < kRedBatch; ++u) {
       sum[0] += v[u][0]; sum[1] += v[u][1]; sum[2] += v[u][2]; sum[3] += v[u][3];
     }
   }
