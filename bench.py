@@ -21,6 +21,7 @@ bounded, time-boxed sample of the same decode steps.
 from __future__ import annotations
 
 import argparse
+import importlib.util
 import json
 import os
 import statistics
@@ -257,16 +258,42 @@ def cpu_baseline(wl_rows, k, n, budget_s: float = 10.0) -> dict:
         if el >= budget_s or steps >= 5000:
             break
     total = steps * sum(bytes_per_call(m, k, n) for m in wl_rows)
-    model = ""
-    try:
-        with open("/proc/cpuinfo") as f:
-            model = next((l.split(":", 1)[1].strip() for l in f if l.startswith("model name")), "")
-    except OSError:
-        pass
+    host = host_cpu_facts()
     return {"value": round(total / el / 1e9, 3), "unit": "GB/s", "cores": threads, "kind": "port",
             "sample": f"{steps} decode steps (M=1,2,4 x 5120 -> 34816) in {el:.1f} s, {threads} OpenMP threads, "
-                      f"oracle/qmm4_cpu.c (fp32 accumulation), CPU: {model}",
-            "ms_per_step": round(el / steps * 1e3, 2)}
+                      f"oracle/qmm4_cpu.c (fp32 accumulation), CPU: {host['model']}",
+            "ms_per_step": round(el / steps * 1e3, 2),
+            "threads_used": threads, "host_cpus_visible": host["visible"], "host_logical_cpus": host["logical"],
+            "host_physical_cores": host["physical"],
+            "mlx_cpu": ("mlx importable but not timed" if importlib.util.find_spec("mlx") is not None
+                        else "mx.quantized_matmul on mx.cpu: mlx is not installed on this host and cannot be "
+                             "installed offline; unavailable")}
+
+
+def host_cpu_facts() -> dict:
+    """The host's CPU model, logical CPUs, CPUs this process may run on, and physical cores
+    (distinct (physical id, core id) pairs of /proc/cpuinfo)."""
+    model, cores, phys, core = "", set(), None, None
+    try:
+        with open("/proc/cpuinfo") as f:
+            for ln in f:
+                key, _, val = ln.partition(":")
+                key, val = key.strip(), val.strip()
+                if key == "model name" and not model:
+                    model = val
+                elif key == "physical id":
+                    phys = val
+                elif key == "core id":
+                    core = val
+                elif not key and phys is not None and core is not None:
+                    cores.add((phys, core))
+                    phys = core = None
+            if phys is not None and core is not None:
+                cores.add((phys, core))
+    except OSError:
+        pass
+    return {"model": model, "logical": os.cpu_count(), "visible": len(os.sched_getaffinity(0)),
+            "physical": len(cores) or None}
 
 
 def profile_mode(torch, lib, dev, args) -> int:

@@ -17,6 +17,9 @@
  *     message for the calling host thread;
  *   - the library keeps one internal workspace per (device, stream) for split-K partial sums;
  *     calls on the same stream are ordered, calls on different streams use different workspaces.
+ *     A workspace that a call used while its stream was being captured into a graph is never
+ *     freed (the graph may replay on it later); a call that would need it to grow during capture
+ *     returns QMM4_ERR_CAPTURE instead of allocating.
  */
 #ifndef MI355X_QMM4_H
 #define MI355X_QMM4_H
@@ -32,6 +35,9 @@ extern "C" {
 #define QMM4_ERR_UNSUPPORTED (-95) /* bits != 4, group_size != 64, transpose == 0       */
 #define QMM4_ERR_NOMEM (-12)       /* workspace allocation failed                       */
 #define QMM4_ERR_HIP (-5)          /* a HIP runtime call failed (message has the name)  */
+#define QMM4_ERR_CAPTURE (-16)     /* a library buffer must grow while the stream is    */
+                                   /* being captured into a graph: call once with that  */
+                                   /* shape on that stream before capturing             */
 
 /*
  * y = x @ dequant(w)^T  — the quantized-matmul call of the verify, decode and prefill passes.

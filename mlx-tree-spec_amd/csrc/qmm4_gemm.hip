@@ -31,10 +31,7 @@ namespace qmm4 {
 namespace {
 
 constexpr int BK = 64, LDK = BK + 8;  // K step; LDS row pitch (bf16) of a K step
-#ifndef QMM4_GEMM_WAVES
-#define QMM4_GEMM_WAVES 8
-#endif
-constexpr int kWaves = QMM4_GEMM_WAVES;  // 4: a 2 x 2 wave grid; 8: 2 x 4
+constexpr int kWaves = 8;  // a 2 x 4 wave grid, two waves per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kWavesN = kWaves / 2;
 constexpr int kGroupM = 4;

@@ -372,6 +372,11 @@ void rowphase_kernel(RowPhaseParams P) {
   };
 
   if (P.S == 1) {
+    // The y tile reuses the x stages. The last phases still issued x DMA (zeros from outside the
+    // buffer) that the phase barrier's count lets run on, so every wave first waits for all of its
+    // loads, and a barrier makes sure no DMA of any wave can still land on the tile.
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    __syncthreads();
     tile_to_lds(acc);
     __syncthreads();
     write_y();
@@ -399,9 +404,6 @@ void rowphase_kernel(RowPhaseParams P) {
 // one CU took 6.5-7.6 us at the end of the batched-verify down projection; spread over the GPU
 // the same bytes take a few microseconds.
 constexpr int kRedThreads = 256;
-#ifndef QMM4_RP_REDUCE_BATCH
-#define QMM4_RP_REDUCE_BATCH 16
-#endif
 template <class C>
 __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhaseParams P) {
   constexpr int MB = C::MB, BPW = C::BPW, kRpWaves = C::kRpWaves;
@@ -426,7 +428,7 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
   // kRedBatch contributors' loads in flight at a time (one memory round trip for the usual S of
   // 10-12); past the last they read zero (an offset outside the buffer), and adding +0 leaves a
   // sum that is not -0 unchanged (a sum from +0 never is -0).
-  constexpr int kRedBatch = QMM4_RP_REDUCE_BATCH;
+  constexpr int kRedBatch = 16;
   for (int q = 0; q < P.S; q += kRedBatch) {
     f32x4 v[kRedBatch];
 #pragma unroll
@@ -492,9 +494,7 @@ static const void* rowphase_func(int id) {
   }
 }
 
-#ifndef QMM4_RP_NARROW_BPW
-#define QMM4_RP_NARROW_BPW 2  // blocks per wave when K is split
-#endif
+constexpr int kRpNarrowBpw = 2;  // blocks per wave when K is split
 
 bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   if (M < 1 || M > 64 || N % 16 != 0 || cus < 1) return false;
@@ -504,10 +504,10 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   // Row offsets of this kernel stay below 2 GiB (rows past the end are addressed at 2 GiB).
   if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 31)) return false;
   // Wide: every CU its own rows over all of K (at least one block per wave). Narrow: ranges of
-  // QMM4_RP_NARROW_BPW blocks per wave, K split over the CUs.
+  // kRpNarrowBpw blocks per wave, K split over the CUs.
   constexpr int kW = 8;  // waves per workgroup of every variant
   const bool wide = NB >= kW * cus;
-  const int want = wide ? ((NB + cus - 1) / cus + kW - 1) / kW : QMM4_RP_NARROW_BPW;
+  const int want = wide ? ((NB + cus - 1) / cus + kW - 1) / kW : kRpNarrowBpw;
   // The variant for mb rows with the fewest blocks per wave that still holds `want` (or the most).
   int id = -1, best_b = 0;
   for (int c = 0; c < kRpVariants; ++c) {

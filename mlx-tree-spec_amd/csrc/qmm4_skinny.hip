@@ -560,24 +560,14 @@ void skinny_kernel(SkinnyParams P) {
 // is at most 16 KB (rows * V <= 64), so larger row counts take shorter steps; V = 2 and 1 also
 // serve K that four super-steps do not divide. Variants 12-14 are the resident-x twins of 0-2
 // (48 KB of x slots each, three workgroups per CU).
-#ifndef QMM4_SKINNY_PF_SMALL
-#define QMM4_SKINNY_PF_SMALL 2  // prefetch depth of the variants for up to 16 rows
-#endif
-#ifndef QMM4_SKINNY_WAVES32
-#define QMM4_SKINNY_WAVES32 12  // 17-32 rows: 192-column tiles, one x staging per 12 waves
-#endif
-#ifndef QMM4_SKINNY_WAVES64
-#define QMM4_SKINNY_WAVES64 4
-#endif
-#ifndef QMM4_SKINNY_PF_RX
-#define QMM4_SKINNY_PF_RX 2     // prefetch depth of the resident-x variants
-#endif
+// Prefetch depth 2 everywhere; 17-32 rows use 12-wave workgroups (192-column tiles, one x staging
+// per 12 waves).
 #define QMM4_SKINNY_VARIANTS(X) \
-  X(0, 4, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0, 4)   \
-  X(1, 8, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0, 4)   \
-  X(2, 16, 4, 1, QMM4_SKINNY_PF_SMALL, 4, 0, 4)  \
-  X(3, 32, 2, 1, 2, 4, 0, QMM4_SKINNY_WAVES32)                     \
-  X(4, 64, 1, 1, 2, 4, 0, QMM4_SKINNY_WAVES64)                     \
+  X(0, 4, 4, 1, 2, 4, 0, 4)   \
+  X(1, 8, 4, 1, 2, 4, 0, 4)   \
+  X(2, 16, 4, 1, 2, 4, 0, 4)  \
+  X(3, 32, 2, 1, 2, 4, 0, 12)                     \
+  X(4, 64, 1, 1, 2, 4, 0, 4)                     \
   X(5, 4, 2, 1, 2, 4, 0, 4)                      \
   X(6, 8, 2, 1, 2, 4, 0, 4)                      \
   X(7, 16, 2, 1, 2, 4, 0, 4)                     \
@@ -585,9 +575,9 @@ void skinny_kernel(SkinnyParams P) {
   X(9, 8, 1, 1, 2, 4, 0, 4)                      \
   X(10, 16, 1, 1, 2, 4, 0, 4)                    \
   X(11, 32, 1, 1, 2, 4, 0, 4)                    \
-  X(12, 4, 4, 1, QMM4_SKINNY_PF_RX, 4, 12, 4)    \
-  X(13, 8, 4, 1, QMM4_SKINNY_PF_RX, 4, 6, 4)     \
-  X(14, 16, 4, 1, QMM4_SKINNY_PF_RX, 4, 3, 4)
+  X(12, 4, 4, 1, 2, 4, 12, 4)    \
+  X(13, 8, 4, 1, 2, 4, 6, 4)     \
+  X(14, 16, 4, 1, 2, 4, 3, 4)
 
 #define QMM4_CFG_TYPE(id, mp, v, ct, pf, wpe, xs, wv) typedef SkinnyCfg<mp, v, ct, pf, wpe, xs, wv> SkCfg##id;
 QMM4_SKINNY_VARIANTS(QMM4_CFG_TYPE)

@@ -433,18 +433,9 @@ static void verify_geometry(int variant, int* cw, int* v, int* threads, size_t* 
   }
 }
 
-#ifndef QMM4_VV1
-#define QMM4_VV1 3
-#endif
-#ifndef QMM4_VV2
-#define QMM4_VV2 1
-#endif
-#ifndef QMM4_VV4
-#define QMM4_VV4 2
-#endif
 int verify_variant(int M, int vmax) {
   const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
-  int id = mb == 1 ? QMM4_VV1 : mb == 2 ? QMM4_VV2 : QMM4_VV4;
+  int id = mb == 1 ? 3 : mb == 2 ? 1 : 2;  // preferred variant per row blocks
   int cw, v, threads;
   size_t lds;
   verify_geometry(id, &cw, &v, &threads, &lds);

@@ -16,6 +16,7 @@ QMM4_ERR_INVALID = -22
 QMM4_ERR_UNSUPPORTED = -95
 QMM4_ERR_NOMEM = -12
 QMM4_ERR_HIP = -5
+QMM4_ERR_CAPTURE = -16
 
 # name -> (restype, argtypes); the symbols include/qmm4.h declares.
 _vp = ctypes.c_void_p

@@ -13,6 +13,7 @@ from __future__ import annotations
 import torch
 
 from . import _lib
+from .qmm import aligned_contiguous
 
 
 def add_rms_norm_(x: torch.Tensor, r: torch.Tensor, weight: torch.Tensor, eps: float):
@@ -29,9 +30,9 @@ def add_rms_norm_(x: torch.Tensor, r: torch.Tensor, weight: torch.Tensor, eps: f
     dev = x.device
     if dev.type != "cuda" or r.device != dev or weight.device != dev:
         raise ValueError("[add_rms_norm] x, r and weight must be on one HIP device; there is no CPU path")
-    x2 = x.reshape(-1, d).contiguous()
-    r2 = r.reshape(-1, d).contiguous()
-    w = weight.contiguous()
+    x2 = aligned_contiguous(x.reshape(-1, d))
+    r2 = aligned_contiguous(r.reshape(-1, d))
+    w = aligned_contiguous(weight)
     h = torch.empty_like(x2)
     n = torch.empty_like(x2)
     lib = _lib.load()

@@ -2,7 +2,8 @@
 
 Mirrors src/mlx_tree_spec/packed_linear.py:
   eligible(mod)        -> packed_linear.eligible (49-58): 4-bit affine with biases, no linear
-                          bias, N % 32 == 0, K % 128 == 0
+                          bias, N % 32 == 0, K % 128 == 0 (and group_size == 64, the one group
+                          size these kernels implement)
   install(model)       -> packed_linear.install (136-179): prepares every eligible module and
                           prebinds its launcher; returns the same summary dict
   QuantizedLinear      -> mlx.nn.QuantizedLinear (weight uint32 [N, K/8], scales and biases
@@ -16,7 +17,8 @@ Differences by design (MI355X-first):
   * no install-time timing race between kernels: the kernel is a fixed function of the row count
     (M <= SKINNY_MAX_ROWS: the HBM-bound skinny kernel; larger M: the MFMA GEMM), decided inside
     the library;
-  * the prebound launcher skips the per-call argument checks (weights were validated once).
+  * the prebound launcher skips the per-call argument checks (weights were validated once); it
+    holds the bound tensors and rebinds when the module's buffers are replaced.
 """
 
 from __future__ import annotations
@@ -27,7 +29,7 @@ from collections import defaultdict
 import torch
 
 from . import _lib
-from .qmm import gate_up_silu, quantized_matmul
+from .qmm import aligned_contiguous, gate_up_silu, quantized_matmul
 
 SKINNY_MAX_ROWS = 64  # rows <= this take the skinny kernel (the reference's PREFILL_M is 64)
 STATS: dict[str, int] = defaultdict(int)
@@ -103,10 +105,16 @@ class QuantizedMLP(torch.nn.Module):
 
 
 def eligible(mod) -> bool:
-    """packed_linear.eligible: the modules the packed kernels take."""
+    """packed_linear.eligible (packed_linear.py:49-58): the modules the packed kernels take.
+
+    One condition more than the reference's: group_size == 64, the only group size the gfx950
+    kernels implement (the reference's kernels take the group size as a parameter). A module
+    with another group size is reported as not packed instead of failing at its first call.
+    """
     return (
         isinstance(mod, QuantizedLinear)
         and mod.bits == 4
+        and mod.group_size == 64
         and getattr(mod, "mode", "affine") == "affine"
         and mod.biases is not None
         and mod.bias is None
@@ -115,21 +123,45 @@ def eligible(mod) -> bool:
     )
 
 
+def _bindable(mod: QuantizedLinear) -> bool:
+    """The module's buffers as a launcher binds them: on a HIP device, bf16 scales and biases,
+    int32/uint32 codes."""
+    return (mod.weight.device.type == "cuda" and mod.weight.dtype in (torch.int32, torch.uint32)
+            and mod.scales.dtype == torch.bfloat16 and mod.biases.dtype == torch.bfloat16
+            and mod.scales.device == mod.weight.device and mod.biases.device == mod.weight.device)
+
+
+def _prepare(mod: QuantizedLinear) -> None:
+    """Make the module's buffers contiguous and 16-byte aligned (copies only where needed)."""
+    for name in ("weight", "scales", "biases"):
+        t = getattr(mod, name)
+        a = aligned_contiguous(t)
+        if a is not t:
+            setattr(mod, name, a)
+
+
 def _launcher(mod: QuantizedLinear):
-    """mod's matmul with weights, shape and library bound: per call only x is checked."""
+    """mod's matmul with weights, shape and library bound: per call only x is checked, plus a
+    cheap test that the bound buffers are still the module's own (the same tensor objects, the
+    same storage, bf16 scales and biases). The closure holds the tensors themselves, so their
+    memory stays valid while it exists; when the module's buffers have been replaced (e.g.
+    mod.to(dtype), a reassigned weight, .data swapped) the launcher returns None and the caller
+    rebinds."""
     w, s, b = mod.weight, mod.scales, mod.biases
     n, k, gs = mod.output_dims, mod.input_dims, mod.group_size
     wp, sp, bp = w.data_ptr(), s.data_ptr(), b.data_ptr()
     dev = w.device
     fn = _lib.load().qmm4_affine_bf16
 
-    def run(x: torch.Tensor) -> torch.Tensor:
+    def run(x: torch.Tensor) -> torch.Tensor | None:
+        if (mod.weight is not w or mod.scales is not s or mod.biases is not b or w.data_ptr() != wp
+                or s.data_ptr() != sp or b.data_ptr() != bp or s.dtype != torch.bfloat16
+                or b.dtype != torch.bfloat16):
+            return None
         if x.dtype != torch.bfloat16 or x.shape[-1] != k or x.device != dev:
             raise ValueError(f"[QuantizedLinear] expected bfloat16 (..., {k}) on {dev}, got "
                              f"{x.dtype} {tuple(x.shape)} on {x.device}")
-        x2 = x.reshape(-1, k)
-        if not x2.is_contiguous() or x2.data_ptr() % 16:
-            x2 = x2.contiguous()
+        x2 = aligned_contiguous(x.reshape(-1, k))
         y = torch.empty((*x.shape[:-1], n), dtype=torch.bfloat16, device=dev)
         rc = fn(x2.data_ptr(), wp, sp, bp, y.data_ptr(), x2.shape[0], n, k, gs, 4, 1,
                 torch.cuda.current_stream(dev).cuda_stream)
@@ -144,9 +176,16 @@ def _call(self: QuantizedLinear, x: torch.Tensor) -> torch.Tensor:
     rows = math.prod(sh[:-1])
     STATS["skinny" if rows <= SKINNY_MAX_ROWS else "gemm"] += 1
     run = self.__dict__.get("_fast")
-    if run is not None:
-        y = run(x)
-    else:
+    y = run(x) if run is not None else None
+    if y is None:
+        if run is not None:
+            # The bound buffers were replaced since install(): rebind to the current ones (or drop
+            # the launcher when they no longer suit it; the checked call below then raises).
+            STATS["rebound"] += 1
+            self.__dict__.pop("_fast")
+            if eligible(self) and _bindable(self):
+                _prepare(self)
+                object.__setattr__(self, "_fast", _launcher(self))
         y = quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                              group_size=self.group_size, bits=self.bits, mode=self.mode)
     if self.bias is not None:
@@ -158,8 +197,9 @@ def install(model: torch.nn.Module, verbose: bool = True) -> dict:
     """Prepare every eligible QuantizedLinear of `model` for the packed kernels.
 
     Weights must already be on the HIP device. Each module's buffers are made contiguous and
-    16-byte aligned once and a launcher with them bound is attached, so a forward's calls skip
-    the generic argument checks. Returns the reference's summary dict.
+    16-byte aligned once (copied only where they are not) and a launcher with them bound is
+    attached, so a forward's calls skip the generic argument checks; a launcher whose buffers
+    were later replaced is rebound at the next call. Returns the reference's summary dict.
     """
     before = torch.cuda.memory_allocated() if torch.cuda.is_available() else 0
     groups: dict[tuple[int, int], int] = defaultdict(int)
@@ -171,10 +211,7 @@ def install(model: torch.nn.Module, verbose: bool = True) -> dict:
             raise ValueError("install(): move the model to the HIP device first")
         if mod.scales.dtype != torch.bfloat16 or mod.biases.dtype != torch.bfloat16:
             raise ValueError("install(): scales and biases must be bfloat16")
-        for name in ("weight", "scales", "biases"):
-            t = getattr(mod, name)
-            if not t.is_contiguous() or t.data_ptr() % 16:
-                setattr(mod, name, t.contiguous())
+        _prepare(mod)
         object.__setattr__(mod, "_fast", _launcher(mod))
         groups[(mod.input_dims, mod.output_dims)] += 1
         packed += 1

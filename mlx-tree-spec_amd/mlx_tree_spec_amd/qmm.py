@@ -63,8 +63,16 @@ def _check_device(what: str, *ts: torch.Tensor) -> torch.device:
     return dev
 
 
-def _contig(t: torch.Tensor) -> torch.Tensor:
-    return t if t.is_contiguous() and t.data_ptr() % 16 == 0 else t.contiguous()
+def aligned_contiguous(t: torch.Tensor, align: int = 16) -> torch.Tensor:
+    """t itself when it is contiguous and its data starts on an `align`-byte boundary, else a copy
+    in fresh storage (the caching allocator's blocks start on 512-byte boundaries). A contiguous
+    view at an odd offset stays at that offset under .contiguous(), which the kernels reject."""
+    if t.is_contiguous() and t.data_ptr() % align == 0:
+        return t
+    out = torch.empty(t.shape, dtype=t.dtype, device=t.device)
+    out.copy_(t)
+    return out
+
 
 
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
@@ -79,11 +87,11 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     k = x.shape[-1]
     n, _ = _check_weights(w, scales, biases, k, group_size, bits, "quantized_matmul")
     dev = _check_device("quantized_matmul", x, w, scales, biases)
-    x2 = _contig(x.reshape(-1, k))
+    x2 = aligned_contiguous(x.reshape(-1, k))
     m = x2.shape[0]
-    w = _contig(w)
-    scales = scales.contiguous()
-    biases = biases.contiguous()
+    w = aligned_contiguous(w)
+    scales = aligned_contiguous(scales)
+    biases = aligned_contiguous(biases)
     y = torch.empty((*x.shape[:-1], n), dtype=torch.bfloat16, device=dev)
     lib = _lib.load()
     with torch.cuda.device(dev):
@@ -113,11 +121,11 @@ def gate_up_silu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases:
     if n % 32:
         raise ValueError(f"[gate_up_silu] w has {n} rows; gate and up halves need a multiple of 32")
     dev = _check_device("gate_up_silu", x, w, scales, biases)
-    x2 = _contig(x.reshape(-1, k))
+    x2 = aligned_contiguous(x.reshape(-1, k))
     m = x2.shape[0]
-    w = _contig(w)
-    scales = scales.contiguous()
-    biases = biases.contiguous()
+    w = aligned_contiguous(w)
+    scales = aligned_contiguous(scales)
+    biases = aligned_contiguous(biases)
     y = torch.empty((*x.shape[:-1], n // 2), dtype=torch.bfloat16, device=dev)
     lib = _lib.load()
     with torch.cuda.device(dev):
@@ -134,9 +142,9 @@ def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, grou
     _check_format(group_size, bits, True, mode)
     n, k = _check_weights(w, scales, biases, None, group_size, bits, "dequantize")
     dev = _check_device("dequantize", w, scales, biases)
-    w = _contig(w)
-    scales = scales.contiguous()
-    biases = biases.contiguous()
+    w = aligned_contiguous(w)
+    scales = aligned_contiguous(scales)
+    biases = aligned_contiguous(biases)
     out = torch.empty((n, k), dtype=torch.bfloat16, device=dev)
     lib = _lib.load()
     with torch.cuda.device(dev):

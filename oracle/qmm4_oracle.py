@@ -11,7 +11,6 @@ Restates, in numpy, the reference's arithmetic for the path:
   * matmul:   y = fp32(x) @ fp32(dequant(w)).T, bf16 out         tests/test_units.py:108 ("exact")
   * metrics:  max|y-ref| / max|ref|                              experiments/qmm_prefill.py:98
   * layouts:  pack_nax / its inverse                            qmm_packed.py:223-232, packed_linear.py:72-80
-  * eligibility gate                                             packed_linear.py:49-58
   * synthetic inputs of the five benchmark workloads (seeded PCG64; draw order fixed here).
 
 bf16 values are carried as raw uint16 bit patterns throughout, so nothing here depends on a
@@ -176,7 +175,7 @@ MAX_REL_TOL = 1e-2
 MEAN_REL_TOL = 2e-3
 
 
-# ----------------------------------------------------------------------------- layouts / gate
+# ----------------------------------------------------------------------------- layouts
 def pack_nax(w, scales, biases):
     """The reference's relayout (qmm_packed.py:223-232): 32-row tiles, 16-wide K blocks.
 
@@ -201,13 +200,6 @@ def unpack_nax(wq2, sp2, bp2, n: int):
     s = np.asarray(sp2).reshape(n // 32, g, 32).transpose(0, 2, 1).reshape(n, g)
     b = np.asarray(bp2).reshape(n // 32, g, 32).transpose(0, 2, 1).reshape(n, g)
     return np.ascontiguousarray(w), np.ascontiguousarray(s), np.ascontiguousarray(b)
-
-
-def eligible_shape(n: int, k: int, bits: int = 4, group_size: int = 64, has_biases: bool = True,
-                   has_bias: bool = False, mode: str = "affine") -> bool:
-    """packed_linear.eligible (packed_linear.py:49-58) on a shape: 4-bit affine with biases, no
-    linear bias, N % 32 == 0 and K % 128 == 0."""
-    return bits == 4 and mode == "affine" and has_biases and not has_bias and n % 32 == 0 and k % 128 == 0
 
 
 # ----------------------------------------------------------------------------- synthetic inputs

@@ -12,6 +12,7 @@ Bars:
 
 import os
 import sys
+import warnings
 
 import numpy as np
 import pytest
@@ -107,7 +108,8 @@ def test_dequant_every_finite_bf16_scale(bias_kind):
     n = s.size
     rng = np.random.default_rng(11)
     if bias_kind == "model":
-        b = O.f32_to_bf16_bits(-8 * O.bf16_bits_to_f32(s) + rng.standard_normal(n).astype(np.float32) * 1e-3)
+        with np.errstate(over="ignore"):  # -8 s overflows for the largest scales; those become 0 below
+            b = O.f32_to_bf16_bits(-8 * O.bf16_bits_to_f32(s) + rng.standard_normal(n).astype(np.float32) * 1e-3)
         b = np.where(((b >> 7) & 0xFF) == 0xFF, np.uint16(0), b)
     else:
         b = rng.integers(0, 65536, n).astype(np.uint16)
@@ -424,20 +426,104 @@ def test_noncontiguous_and_empty():
 
 
 def test_quantized_linear_install():
+    """The prebound launcher of install() against the oracle (not only against the library's own
+    unbound call), at decode, verify and prefill row counts."""
     k, n = 1024, 256
-    mods = []
+    mods, wts = [], []
     for seed in range(3):
         _, w, s, b = O.make_inputs(1, k, n, seed=seed)
         mods.append(QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(s), bf16_dev(b)))
+        wts.append((w, s, b))
     model = torch.nn.Sequential(*mods)
     summary = install(model, verbose=False)
     assert summary["packed"] == 3
+    assert all("_fast" in m.__dict__ for m in mods)
     for m in (1, 16, 100):
         x, *_ = O.make_inputs(m, k, n, seed=m)
         xd = bf16_dev(x).reshape(1, m, k)
-        before = dict(STATS)
-        y = mods[0](xd)
-        key = "skinny" if m <= 64 else "gemm"
-        assert STATS[key] == before.get(key, 0) + 1
-        ref = quantized_matmul(xd, mods[0].weight, mods[0].scales, mods[0].biases)
-        assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+        for i in (0, 2):
+            before = dict(STATS)
+            y = mods[i](xd)
+            key = "skinny" if m <= 64 else "gemm"
+            assert STATS[key] == before.get(key, 0) + 1
+            assert STATS["rebound"] == before.get("rebound", 0)
+            assert tuple(y.shape) == (1, m, n)
+            check_qmm(host_bits(y).reshape(m, n), O.quantized_matmul_exact(x, *wts[i]), f"install M={m} mod={i}",
+                      (x, *wts[i]))
+            ref = quantized_matmul(xd, mods[i].weight, mods[i].scales, mods[i].biases)
+            assert torch.equal(y.view(torch.int16), ref.view(torch.int16))
+
+
+def test_install_rebinds_replaced_buffers():
+    """A launcher whose module's buffers were replaced after install() rebinds to the new ones (no
+    read of the freed tensors), and a dtype the kernels cannot take raises."""
+    k, n = 512, 128
+    _, w, s, b = O.make_inputs(1, k, n, seed=21)
+    mod = QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(s), bf16_dev(b))
+    install(mod, verbose=False)
+    x, *_ = O.make_inputs(4, k, n, seed=22)
+    check_qmm(host_bits(mod(bf16_dev(x))), O.quantized_matmul_exact(x, w, s, b), "bound", (x, w, s, b))
+    _, w2, s2, b2 = O.make_inputs(1, k, n, seed=23)
+    mod.weight, mod.scales, mod.biases = u32_dev(w2), bf16_dev(s2), bf16_dev(b2)
+    torch.cuda.synchronize()
+    before = STATS["rebound"]
+    check_qmm(host_bits(mod(bf16_dev(x))), O.quantized_matmul_exact(x, w2, s2, b2), "rebound", (x, w2, s2, b2))
+    assert STATS["rebound"] == before + 1 and "_fast" in mod.__dict__
+    mod.to(torch.float32)  # scales and biases become fp32 tensors
+    with pytest.raises(ValueError):
+        mod(bf16_dev(x))
+
+
+def test_misaligned_contiguous_inputs():
+    """Contiguous views that start 2 bytes past a 16-byte boundary (accepted by MLX) are copied to
+    aligned storage by the Python layer instead of being rejected by the C ABI."""
+    m, k, n = 5, 1024, 256
+    x, w, s, b = O.make_inputs(m, k, n, seed=31)
+    xs = bf16_dev(np.concatenate([np.zeros(1, np.uint16), x.reshape(-1)]))[1:].view(m, k)
+    ss = bf16_dev(np.concatenate([np.zeros(1, np.uint16), s.reshape(-1)]))[1:].view(n, k // 64)
+    bs = bf16_dev(np.concatenate([np.zeros(1, np.uint16), b.reshape(-1)]))[1:].view(n, k // 64)
+    assert xs.is_contiguous() and xs.data_ptr() % 16 == 2 and ss.data_ptr() % 16 == 2
+    y = quantized_matmul(xs, u32_dev(w), ss, bs)
+    check_qmm(host_bits(y), O.quantized_matmul_exact(x, w, s, b), "misaligned", (x, w, s, b))
+    from mlx_tree_spec_amd import add_rms_norm_
+    wn = bf16_dev(np.full(k, 0x3F80, np.uint16))
+    h, nn = add_rms_norm_(xs, xs, wn, 1e-6)
+    ho, no = O.add_rms_norm(x, x, np.full(k, 0x3F80, np.uint16), 1e-6)
+    assert np.array_equal(host_bits(h), ho)
+
+
+def test_capture_needs_existing_workspace():
+    """Under graph capture a call that would have to allocate its split-K workspace returns
+    QMM4_ERR_CAPTURE; after one eager call on the stream the same call captures and replays."""
+    from mlx_tree_spec_amd import _lib
+    x, w, s, b = O.make_inputs(16, 5120, 512, seed=41)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = torch.empty((16, 512), dtype=torch.bfloat16, device=DEV)
+    lib = _lib.load()
+    st = torch.cuda.Stream()
+    g = torch.cuda.CUDAGraph()
+    rc = None
+    try:
+        with warnings.catch_warnings():
+            warnings.simplefilter("ignore")  # the refused call leaves the captured graph empty
+            with torch.cuda.graph(g, stream=st):
+                rc = lib.qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(),
+                                          y.data_ptr(), 16, 512, 5120, 64, 4, 1, st.cuda_stream)
+    except RuntimeError:
+        pass  # an empty or invalidated capture may fail to instantiate
+    assert rc == _lib.QMM4_ERR_CAPTURE, rc
+    torch.cuda.synchronize()
+    with torch.cuda.stream(st):
+        assert lib.qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), y.data_ptr(),
+                                    16, 512, 5120, 64, 4, 1, st.cuda_stream) == 0
+    st.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g, stream=st):
+        assert lib.qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), y.data_ptr(),
+                                    16, 512, 5120, 64, 4, 1, st.cuda_stream) == 0
+    ref = O.quantized_matmul_exact(x, w, s, b)
+    for rep in range(3):
+        y.zero_()
+        g.replay()
+        torch.cuda.synchronize()
+        check_qmm(host_bits(y), ref, f"captured replay {rep}", (x, w, s, b))

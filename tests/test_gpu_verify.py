@@ -94,17 +94,34 @@ def test_stack_tail_matches_oracle_composition(rows):
         assert O.max_rel(g, w) <= O.MAX_REL_TOL and O.mean_rel(g, w) <= O.MEAN_REL_TOL
 
 
+def check_tail(got, want, what):
+    for gt_, wt in zip(got, want):
+        g = O.bf16_bits_to_f32(host_bits(gt_)).astype(np.float64)
+        w = O.bf16_bits_to_f32(wt).astype(np.float64)
+        print(f"  {what}: max_rel={O.max_rel(g, w):.2e} mean_rel={O.mean_rel(g, w):.2e}", flush=True)
+        assert O.max_rel(g, w) <= O.MAX_REL_TOL and O.mean_rel(g, w) <= O.MEAN_REL_TOL
+
+
 @pytest.mark.parametrize("rows", [4, 64])
 def test_graphed_tail_replays_equal_eager(rows):
-    layers, final, _, _ = make_stack(seed=1)
+    """Replays against the oracle's composition (not only against eager calls), with eager work of
+    the same shape and of a larger shape on other streams between the replays."""
+    layers, final, ref, wfinal = make_stack(seed=1)
     gt = GraphedTail(layers, final, rows, D, DEV)
+    side = torch.cuda.Stream()
     for rep in range(3):
         h, rs = inputs(rows, len(layers), 1000 * rows + rep)
         hd, rsd = bf16_dev(h), [bf16_dev(r) for r in rs]
         he, xe = stack_tail(hd, rsd, layers, final)  # eager work between the replays
         he, xe = host_bits(he), host_bits(xe)
+        # A larger batch on another stream: its split-K workspace and scratch are that stream's.
+        hb, rsb = inputs(2 * rows + 7, len(layers), 7 + rep)
+        with torch.cuda.stream(side):
+            stack_tail(bf16_dev(hb), [bf16_dev(r) for r in rsb], layers, final)
+        side.synchronize()
         torch.cuda.synchronize()
         hr, xr = gt(hd, rsd)
         torch.cuda.synchronize()
         assert np.array_equal(host_bits(hr), he), f"replay {rep}: h differs from eager"
         assert np.array_equal(host_bits(xr), xe), f"replay {rep}: x differs from eager"
+        check_tail((hr, xr), oracle_stack(h, rs, ref, wfinal), f"replay {rep} rows={rows} vs oracle")

@@ -67,6 +67,7 @@ def test_quantized_linear_module_and_gate():
     assert not eligible(QuantizedLinear(256, 48))           # N % 32 != 0
     assert not eligible(QuantizedLinear(192, 64))           # K % 128 != 0
     assert not eligible(QuantizedLinear(256, 64, bias=True))
+    assert not eligible(QuantizedLinear(256, 64, group_size=32))  # the kernels implement group 64 only
     b8 = QuantizedLinear(256, 64)
     b8.bits = 8
     assert not eligible(b8)
