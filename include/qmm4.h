@@ -61,6 +61,24 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
                      int transpose, void* hip_stream);
 
 /*
+ * y = x @ dequant(w)^T without any allocation: the same checks, kernels and results (bit for bit)
+ * as qmm4_affine_bf16, with the split-K workspace in a static device array of
+ * QMM4_NOALLOC_SCRATCH_BYTES per GPU (64 KiB of counters, the rest fp32 partial sums) instead of a
+ * library allocation. It has no counterpart in the reference: it is for callers that cannot
+ * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ *   - Calls no hipMalloc / hipFree / allocating routine. The first call on a device looks the array
+ *     up and clears its counters on `hip_stream` (that call must not be captured:
+ *     QMM4_ERR_CAPTURE); later calls on that device may be captured.
+ *   - A shape whose split-K buffers exceed the array returns QMM4_ERR_INVALID with the sizes.
+ *   - Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different
+ *     streams, or threads without ordering between them) race. Order them on one stream.
+ */
+#define QMM4_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+int qmm4_affine_bf16_noalloc(const void* x, const uint32_t* w, const void* scales, const void* biases,
+                             void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
+                             int transpose, void* hip_stream);
+
+/*
  * y = silu(x @ dequant(w_gate)^T) * (x @ dequant(w_up)^T) — a fused gate+up projection with the
  * SiLU·mul epilogue, the input of down_proj in the MLP of the verify forward
  * (src/mlx_tree_spec/tree_verify.py:446: layer.mlp(x) = down_proj(silu(gate_proj(x)) * up_proj(x));

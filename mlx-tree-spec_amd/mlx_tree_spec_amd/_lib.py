@@ -24,6 +24,7 @@ _i64 = ctypes.c_int64
 _int = ctypes.c_int
 SIGNATURES = {
     "qmm4_affine_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp]),
+    "qmm4_affine_bf16_noalloc": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "qmm4_gate_up_silu_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "dequant4_affine_bf16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp]),
     "qmm4_add_rms_norm_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),

@@ -20,8 +20,9 @@ def declared_functions():
 
 
 def test_header_declares_expected_api():
-    assert declared_functions() == sorted(["qmm4_affine_bf16", "qmm4_gate_up_silu_bf16", "dequant4_affine_bf16",
-                                           "qmm4_add_rms_norm_bf16", "qmm4_last_error", "qmm4_abi_version"])
+    assert declared_functions() == sorted(["qmm4_affine_bf16", "qmm4_affine_bf16_noalloc", "qmm4_gate_up_silu_bf16",
+                                           "dequant4_affine_bf16", "qmm4_add_rms_norm_bf16", "qmm4_last_error",
+                                           "qmm4_abi_version"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -54,6 +55,22 @@ def call(M=4, N=32, K=128, gs=64, bits=4, transpose=1, ptr=0x10000, y=0x20000):
 ])
 def test_qmm_rejects(kw, code, msg):
     assert call(**kw) == code
+    assert msg in _lib.last_error()
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(bits=8), _lib.QMM4_ERR_UNSUPPORTED, "bits=8"),
+    (dict(K=192), _lib.QMM4_ERR_INVALID, "K=192"),
+    (dict(ptr=0x10008), _lib.QMM4_ERR_INVALID, "16-byte aligned"),
+])
+def test_noalloc_rejects_like_qmm(kw, code, msg):
+    """The no-allocation entry point makes the same checks before touching the device."""
+    lib = _lib.load()
+    a = dict(M=4, N=32, K=128, gs=64, bits=4, transpose=1, ptr=0x10000, y=0x20000)
+    a.update(kw)
+    rc = lib.qmm4_affine_bf16_noalloc(a["ptr"], a["ptr"], a["ptr"], a["ptr"], a["y"], a["M"], a["N"], a["K"],
+                                      a["gs"], a["bits"], a["transpose"], None)
+    assert rc == code
     assert msg in _lib.last_error()
 
 
