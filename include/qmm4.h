@@ -50,11 +50,12 @@ extern "C" {
  *   w, x and y each below 4 GiB (with 256 rows of margin: (N + 256) * K / 2, (M + 256) * K * 2 and
  *   (M + 256) * N * 2 bytes below 2^32), x and w 16-byte aligned, scales and biases
  *   4-byte aligned, y 2-byte aligned. M == 0 or N == 0 is a no-op. Rows M <= 64 run one of the
- *   HBM-bound verify/decode kernels (row-split for M <= 4 over a large N or a long K, row-phase for more than
- *   16 rows, a large N, or fewer rows when its K split fills half the CUs, K-split verify or
- *   stream-K skinny otherwise), larger M the MFMA GEMM; the
- *   choice is a fixed function of the shape and the scale/bias alignment. Results are deterministic
- *   (bit-identical across calls and streams).
+ *   HBM-bound verify/decode kernels (row-split for M <= 8 when its plan fits: whole K or a few K
+ *   slices per workgroup, every unit in flight at once for small problems; row-phase for more
+ *   than 16 rows, a large N, or fewer rows when its K split fills half the CUs; K-split verify or
+ *   stream-K skinny otherwise), larger M the MFMA GEMM; the choice is a fixed function of the
+ *   shape and the scale/bias alignment. Results are deterministic (bit-identical across calls and
+ *   streams).
  */
 int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
                      void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,

@@ -75,8 +75,11 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan);
 hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, int M, int N, int K, hipStream_t stream);
 
-// Row-split decode kernel (up to 4 rows, output columns split evenly over one workgroup per CU).
+// Row-split kernel (up to 16 rows, output columns split evenly over one workgroup per CU, K whole
+// or in a few slices).
 struct RowSplitPlan {
+  int MP;       // x rows per A fragment (4 or 8)
+  bool small;   // every unit in flight from the start, all of x in LDS, sums in registers
   int V;        // super-steps (128 k) per unit
   bool fused;   // fused gate+up: y = silu(x w_gate^T) * (x w_up^T), w = [w_gate; w_up]
   int Nout;     // output columns (N, or N / 2 when fused)

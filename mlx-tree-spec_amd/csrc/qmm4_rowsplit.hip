@@ -1,10 +1,11 @@
-// Row-split decode kernel for up to 4 rows of x and many output columns: y = x @ dequant(w)^T.
+// Row-split kernel for up to 8 rows of x and many output columns: y = x @ dequant(w)^T.
 //
 // Same arithmetic and operand layout as the skinny kernel (qmm4_skinny.hip; replaces the
-// reference's qmv_packed and 8/16-row NAX kernels for decode, src/mlx_tree_spec/qmm_packed.py:
-// 151-220, 428-557), with a decomposition for the case where the output columns alone fill the
-// GPU: workgroup p (one per CU, 16 waves) owns the R consecutive weight rows [p R, p R + R) over
-// the whole of K, so workgroups share nothing and no partial sums leave a CU.
+// reference's qmv_packed and 8-row NAX kernels for decode and small verify batches,
+// src/mlx_tree_spec/qmm_packed.py:151-220, 428-557), with a decomposition for the case where the
+// output columns alone fill the GPU: workgroup p (one per CU, 16 waves) owns the R consecutive
+// weight rows [p R, p R + R) over the whole of K, so workgroups share nothing and no partial sums
+// leave a CU.
 //
 //  * Work units: the RB = ceil(R / 16) row blocks x SU = K / (128 V) steps of V super-steps (128 k)
 //    each; unit u = b * SU + st. Waves take units from a counter in LDS as they free up, with
@@ -19,15 +20,19 @@
 //    so each row is read as one contiguous run per unit. Rows past the workgroup's range read as
 //    zero (an offset outside the buffer resource), as do fetches past the last unit (a zero-length
 //    resource).
-//  * x (M <= 4 rows, whole K) is staged once in LDS in A-fragment order. Every wave issues its x
-//    loads before any wave issues a weight fetch (a bare barrier between the two), and the stores
-//    wait for the x loads alone (the vector memory counter is in order).
+//  * x (M <= MP rows, MP = 4 or 8, whole K or the workgroup's K slice) is staged once in LDS in
+//    A-fragment order. Every wave issues its x loads before any wave issues a weight fetch (a bare
+//    barrier between the two), and the stores wait for the x loads alone (the vector memory
+//    counter is in order).
 //  * Dequantization: dequant_word_fast, or dequant_word for a unit in which one of the wave's
 //    rows has a scale outside the fast form's range (a wave-uniform branch per unit).
-//  * Each unit's fp32 sums (MFMA 16x16x32, bf16 inputs) go to their own LDS slot: only lanes
-//    g = 0 hold x rows 0..3, so a slot is 16 lanes x 16 bytes. After one barrier the workgroup adds
-//    the slots of each block in step order (deterministic whatever wave ran which unit) and
-//    writes bf16 y.
+//  * Each unit's fp32 sums (MFMA 16x16x32, bf16 inputs; output row 4 g + r in lane group g) go to
+//    their own LDS slot, the MP / 4 lane groups g < MP / 4 of 16 lanes x 16 bytes. After one
+//    barrier the workgroup adds the slots of each block in step order (deterministic whatever
+//    wave ran which unit) and writes bf16 y.
+//  * Small problems (every unit fits the waves' rings at once, all of x fits LDS): the SMALL form
+//    fetches every unit at the start, loads x straight into LDS behind those fetches, and keeps
+//    each wave's two unit sums in registers until x is dead; the slots then take the x area.
 //  * Fused gate+up (FUSED): w is [w_gate; w_up] (N rows, up rows from N / 2), y is [M, N / 2] =
 //    silu(x @ w_gate^T) * (x @ w_up^T). Workgroup p owns output columns [p R, p R + R); its 2R
 //    weight rows are listed gate rows first, then the up rows of the same columns (N / 2 further),
@@ -46,9 +51,15 @@ namespace {
 
 constexpr int kRsWaves = 16;
 constexpr int kRsThreads = 64 * kRsWaves;
-constexpr int kRsMP = 4;  // x rows held per fragment (M <= 4)
+// MP: x rows held per A fragment (4 or 8; M <= MP). The MFMA's 16 rows are x rows
+// min(row, M - 1); output rows 4 g + r lie in lane group g, so a unit's sums live in the MP / 4
+// lane groups g < MP / 4.
 constexpr int kRsPF = 2;  // units in flight per wave
 constexpr int kRsXB = 4;  // x pieces per thread per staging batch
+// SMALL plans: each wave holds at most kRsPF units for the whole launch, and all of x (at most
+// kRsSmallXP 16-byte pieces per thread: the whole LDS) is loaded global -> LDS directly.
+constexpr int kRsSmallXP = 10;
+constexpr size_t kRsLds = 160 * 1024;
 
 struct RowSplitParams {
   const uint16_t* x;
@@ -89,22 +100,32 @@ __device__ __forceinline__ Scales<V> load_scales(__amdgpu_buffer_rsrc_t r, uint3
   return o;
 }
 
-// Dynamic LDS: x pieces [S][16][kRsMP] (A-fragment order), unit slots [U][16] f32x4, a spare
+// Dynamic LDS: x pieces [S][16][MP] (A-fragment order), unit slots [U][MP / 4][16] f32x4, a spare
 // 16-byte slot (the target of surplus x pieces, so that every x store is unconditional), the counter.
-__host__ __device__ inline size_t rowsplit_xs_bytes(int K) { return (size_t)(K >> 7) * 16 * kRsMP * 16; }
-__host__ __device__ inline size_t rowsplit_part_bytes(int units) { return (size_t)units * 16 * 16; }
+__host__ __device__ inline size_t rowsplit_xs_bytes(int K, int MP) { return (size_t)(K >> 7) * 16 * MP * 16; }
+__host__ __device__ inline size_t rowsplit_part_bytes(int units, int MP) { return (size_t)units * (MP / 4) * 16 * 16; }
 
 // KSPLIT: K in P.KS slices (false: whole K, the slice arithmetic and the merge compiled out).
-template <int V, bool FUSED, bool KSPLIT>
+// SMALL: a problem whose units all fit the waves' rings at once (U <= 32): wave w computes units
+// w and w + 16, both fetched at the start, then x goes straight into LDS; the sums stay in
+// registers until every wave is past its last x read and then take the unit slots over the x
+// area. Every load of such a launch is in flight from the start, which is what bounds small
+// problems (decode and small verify batches over a small N, e.g. 1-8 x 5120 x 5120).
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
+  static_assert(MP == 4 || MP == 8, "x rows per fragment");
+  static_assert(!SMALL || (!FUSED && !KSPLIT), "small plans are plain whole-K projections");
+  constexpr int G = MP / 4;  // lane groups holding output rows
+  typedef f32x4 RowSums[G];  // the sums of one output column over x rows 4 g + r
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
   const int S = P.Kp >> 7;  // super-steps per row in this workgroup's K slice
   const int SU = P.SU;
   const int U = P.RB * SU;
   u32x4* xs = reinterpret_cast<u32x4*>(lds);
-  f32x4* part = reinterpret_cast<f32x4*>(lds + rowsplit_xs_bytes(P.Kp));
-  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.Kp) + rowsplit_part_bytes(U));
+  // SMALL: the slots take over the x area once x is dead.
+  f32x4* part = reinterpret_cast<f32x4*>(lds + (SMALL ? 0 : rowsplit_xs_bytes(P.Kp, MP)));
+  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.Kp, MP) + rowsplit_part_bytes(U, MP));
   int* next = reinterpret_cast<int*>(spare + 1);
 
   const int tid = threadIdx.x;
@@ -120,7 +141,7 @@ void rowsplit_kernel(RowSplitParams P) {
   const int KG = P.K >> 6;
 
   // x pieces: item i = sq * M + m is the 16-byte piece sq (k = 8 sq .. 8 sq + 7) of row m, stored
-  // at LDS position sq * kRsMP + m. All batches but the last are staged before any weight fetch;
+  // at LDS position sq * MP + m. All batches but the last are staged before any weight fetch;
   // the last batch is loaded before the first fetches and stored after them. Loads past the last
   // item go to an offset outside the buffer resource (zeros, no memory access); the stores are
   // unconditional (surplus pieces go to the spare slot): a store under a branch would let the
@@ -145,15 +166,35 @@ void rowsplit_kernel(RowSplitParams P) {
     for (int j = 0; j < kRsXB; ++j) {
       const int i = tid + (batch * kRsXB + j) * kRsThreads;
       const int sq = i / P.M, m = i - sq * P.M;
-      u32x4* dst = i < xitems ? xs + (sq * kRsMP + m) : spare;
+      u32x4* dst = i < xitems ? xs + (sq * MP + m) : spare;
       *dst = xr[j];
     }
   };
-  for (int bt = 0; bt + 1 < nxb; ++bt) {
-    load_x(bt);
-    store_x(bt);
+  // SMALL: x straight into LDS (buffer loads with the LDS bit): LDS slot q = sq * MP + m holds
+  // piece sq of row m, rows m >= M read as zero. A wave's instruction fills 64 consecutive slots
+  // (the instruction's base + 16 lane); the slot count S * 16 * MP is a multiple of 64, so a wave
+  // either fills whole slots or skips the instruction.
+  typedef __attribute__((address_space(3))) void* lds_ptr;
+  auto dma_x_all = [&]() __attribute__((always_inline)) {
+    const int slots = S * 16 * MP;
+#pragma unroll
+    for (int j = 0; j < kRsSmallXP; ++j) {
+      const int base = j * kRsThreads + 64 * wave;
+      if (base < slots) {
+        const int q = base + lane;
+        const int sq = q / MP, m = q - sq * MP;
+        const uint32_t off = m < P.M ? ((uint32_t)m * (uint32_t)P.K + (uint32_t)sq * 8u) * 2u : 0x80000000u;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rx, (lds_ptr)(lds + (size_t)base * 16), 16, off, 0, 0, 0);
+      }
+    }
+  };
+  if constexpr (!SMALL) {
+    for (int bt = 0; bt + 1 < nxb; ++bt) {
+      load_x(bt);
+      store_x(bt);
+    }
+    load_x(nxb - 1);
   }
-  load_x(nxb - 1);
   // Every wave's x loads enter the CU's memory pipeline before any weight fetch: the pipeline
   // returns data in order, so an x load queued behind other waves' fetches would wait for them.
   // (A bare s_barrier: no fence, so no wait for the loads themselves.)
@@ -205,8 +246,15 @@ void rowsplit_kernel(RowSplitParams P) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  store_x(nxb - 1);
-  if (tid == 0) *next = kRsPF * kRsWaves;
+  if constexpr (SMALL) {
+    // The weights (from HBM, the longest latency) went out first; x follows from L2. Every wave
+    // waits for all of its loads, then the barrier publishes x.
+    dma_x_all();
+    asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+  } else {
+    store_x(nxb - 1);
+    if (tid == 0) *next = kRsPF * kRsWaves;
+  }
   __syncthreads();
   if constexpr (KSPLIT) {
     fetch(0, ua);
@@ -214,13 +262,13 @@ void rowsplit_kernel(RowSplitParams P) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  const int aoff = g * 4 * kRsMP + min(n, P.M - 1);
+  const int aoff = g * 4 * MP + min(n, P.M - 1);
   int ndone = 0;
   __builtin_amdgcn_s_setprio(3);
 
   auto compute = [&](int j, int st, auto fast) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast)::value;
-    const u32x4* xb = xs + (size_t)st * V * 16 * kRsMP;
+    const u32x4* xb = xs + (size_t)st * V * 16 * MP;
     f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int v = 0; v < V; ++v) {
@@ -233,7 +281,7 @@ void rowsplit_kernel(RowSplitParams P) {
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt) {
         const u32x4 B = FAST ? dequant_word_fast(wv[j][v][tt], c1, c2, bf) : dequant_word(wv[j][v][tt], c1, c2, bf);
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xb[(v * 16 + tt) * kRsMP + aoff]), as_bf16x8(B), acc,
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xb[(v * 16 + tt) * MP + aoff]), as_bf16x8(B), acc,
                                                       0, 0, 0);
       }
     }
@@ -259,7 +307,7 @@ void rowsplit_kernel(RowSplitParams P) {
       acc = compute(j, st, std::true_type{});
     else
       acc = compute(j, st, std::false_type{});
-    if (g == 0) part[u * 16 + n] = acc;
+    if (g < G) part[(u * G + g) * 16 + n] = acc;
     ++ndone;
     // A wave's issue priority falls with the units it has done: the SIMD arbiter otherwise
     // favours the oldest wave, which then takes most units while the youngest holds its ring's
@@ -271,32 +319,61 @@ void rowsplit_kernel(RowSplitParams P) {
     fetch(j, u);
   };
 
-  for (;;) {
-    if (ua >= U) break;
-    unit(ua, std::integral_constant<int, 0>{});
-    if (ub >= U) break;
-    unit(ub, std::integral_constant<int, 1>{});
+  if constexpr (SMALL) {
+    // Units w and w + 16 (both in the ring since the start), sums kept until x is dead.
+    auto unit_sums = [&](int u, auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      const int st = u - (u / SU) * SU;
+      bool bad = false;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int e2 = 2 * v + (g >> 1);
+        bad |= !fast_scale_ok((sv[j].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
+      }
+      if (__builtin_amdgcn_ballot_w64(bad) == 0) return compute(j, st, std::true_type{});
+      return compute(j, st, std::false_type{});
+    };
+    f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
+    if (ua < U) acc0 = unit_sums(ua, std::integral_constant<int, 0>{});
+    if (ub < U) acc1 = unit_sums(ub, std::integral_constant<int, 1>{});
+    __syncthreads();
+    if (g < G) {
+      if (ua < U) part[(ua * G + g) * 16 + n] = acc0;
+      if (ub < U) part[(ub * G + g) * 16 + n] = acc1;
+    }
+  } else {
+    for (;;) {
+      if (ua >= U) break;
+      unit(ua, std::integral_constant<int, 0>{});
+      if (ub >= U) break;
+      unit(ub, std::integral_constant<int, 1>{});
+    }
   }
   __syncthreads();
 
-  // y[m, col] = sum over the block's steps, in step order, of its unit slots; lane element m of a
-  // slot is x row m. Fused: the same for the column's gate and up blocks, then silu * up.
+  // y[m, col] = sum over the block's steps, in step order, of its unit slots; element r of a slot's
+  // lane group g is x row 4 g + r. Fused: the same for the column's gate and up blocks, then
+  // silu * up.
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
       P.y, 0, rsrc_bytes((unsigned long long)P.M * P.Nout * 2), kBufferRsrcWord3);
-  auto row_sum = [&](int lrow) __attribute__((always_inline)) {
+  auto row_sum = [&](int lrow, RowSums& sum) __attribute__((always_inline)) {
     const int b = lrow >> 4, nn = lrow & 15;
-    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
-    for (int st = 0; st < SU; ++st) {
-      const f32x4 c = part[(b * SU + st) * 16 + nn];
-      sum[0] += c[0]; sum[1] += c[1]; sum[2] += c[2]; sum[3] += c[3];
-    }
-    return sum;
-  };
-  auto write = [&](int col, const f32x4& sum, const f32x4& sup) __attribute__((always_inline)) {
 #pragma unroll
-    for (int m = 0; m < kRsMP; ++m)
+    for (int gg = 0; gg < G; ++gg) sum[gg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int st = 0; st < SU; ++st) {
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const f32x4 c = part[((b * SU + st) * G + gg) * 16 + nn];
+        sum[gg][0] += c[0]; sum[gg][1] += c[1]; sum[gg][2] += c[2]; sum[gg][3] += c[3];
+      }
+    }
+  };
+  auto write = [&](int col, const RowSums& sum, const RowSums& sup) __attribute__((always_inline)) {
+#pragma unroll
+    for (int m = 0; m < MP; ++m)
       if (m < P.M) {
-        const uint32_t o = FUSED ? silu_mul_bf16(bf16_rne(sum[m]), bf16_rne(sup[m])) : bf16_rne(sum[m]);
+        const float v = sum[m >> 2][m & 3];
+        const uint32_t o = FUSED ? silu_mul_bf16(bf16_rne(v), bf16_rne(sup[m >> 2][m & 3])) : bf16_rne(v);
         __builtin_amdgcn_raw_buffer_store_b16((uint16_t)o, ry, (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
       }
   };
@@ -304,7 +381,10 @@ void rowsplit_kernel(RowSplitParams P) {
     for (int c = tid; c < P.R; c += kRsThreads) {
       const int col = r0 + c;
       if (col >= r1) continue;
-      write(col, row_sum(c), FUSED ? row_sum(P.R + c) : f32x4{});
+      RowSums sum, sup;
+      row_sum(c, sum);
+      if (FUSED) row_sum(P.R + c, sup);
+      write(col, sum, sup);
     }
     return;
   }
@@ -313,10 +393,15 @@ void rowsplit_kernel(RowSplitParams P) {
   // column range add the slices in slice order (the same bits whichever arrives last).
   const int RR = FUSED ? 2 * P.R : P.R;
   const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
-      P.part, 0, rsrc_bytes((unsigned long long)gridDim.x * RR * 16), kBufferRsrcWord3);
-  for (int lrow = tid; lrow < RR; lrow += kRsThreads)
-    __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, row_sum(lrow)), rp,
-                                           ((uint32_t)blockIdx.x * RR + lrow) * 16u, 0, kCoherent);
+      P.part, 0, rsrc_bytes((unsigned long long)gridDim.x * RR * G * 16), kBufferRsrcWord3);
+  for (int lrow = tid; lrow < RR; lrow += kRsThreads) {
+    RowSums sum;
+    row_sum(lrow, sum);
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg)
+      __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, sum[gg]), rp,
+                                             (((uint32_t)blockIdx.x * RR + lrow) * G + gg) * 16u, 0, kCoherent);
+  }
   asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   __syncthreads();
   if (tid == 0) {
@@ -325,36 +410,75 @@ void rowsplit_kernel(RowSplitParams P) {
   }
   __syncthreads();
   if (*next == 0) return;
-  auto slice_sum = [&](int lrow) __attribute__((always_inline)) {
-    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  auto slice_sum = [&](int lrow, RowSums& sum) __attribute__((always_inline)) {
+#pragma unroll
+    for (int gg = 0; gg < G; ++gg) sum[gg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int qq = 0; qq < P.KS; ++qq) {
-      const f32x4 c = __builtin_bit_cast(
-          f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, ((uint32_t)(range * P.KS + qq) * RR + lrow) * 16u, 0,
-                                                       kCoherent));
-      sum[0] += c[0]; sum[1] += c[1]; sum[2] += c[2]; sum[3] += c[3];
+#pragma unroll
+      for (int gg = 0; gg < G; ++gg) {
+        const f32x4 c = __builtin_bit_cast(
+            f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, (((uint32_t)(range * P.KS + qq) * RR + lrow) * G + gg) * 16u,
+                                                         0, kCoherent));
+        sum[gg][0] += c[0]; sum[gg][1] += c[1]; sum[gg][2] += c[2]; sum[gg][3] += c[3];
+      }
     }
-    return sum;
   };
   for (int c = tid; c < P.R; c += kRsThreads) {
     const int col = r0 + c;
     if (col >= r1) continue;
-    write(col, slice_sum(c), FUSED ? slice_sum(P.R + c) : f32x4{});
+    RowSums sum, sup;
+    slice_sum(c, sum);
+    if (FUSED) slice_sum(P.R + c, sup);
+    write(col, sum, sup);
   }
   if (tid == 0) __hip_atomic_store(&P.cnt[range], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 }  // namespace
 
+int rowsplit_mp(int M) { return M <= 4 ? 4 : 8; }
+
 bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan) {
-  if (M < 1 || M > kRsMP || cus < 1) return false;
+  if (M < 1 || M > 8 || cus < 1) return false;
   if (fused && N % 32 != 0) return false;
   // Row offsets of this kernel stay below 1 GiB.
   if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 30)) return false;
+  const int MP = rowsplit_mp(M);
   const int nout = fused ? N / 2 : N;
-  // Whole K per workgroup when the columns alone give every CU at least 4 row blocks; otherwise
-  // K in 2 or 4 slices over as many workgroups per column range, when each workgroup still has
-  // at least 3 units per wave.
-  for (int ks = 1; ks <= 4; ks *= 2) {
+  // Up to 4 rows: whole K per workgroup when the columns alone give every CU at least 4 row
+  // blocks; otherwise K in 2 or 4 slices over as many workgroups per column range, when each
+  // workgroup still has at least 3 units per wave. 5 to 8 rows (a small verify batch): the fewest
+  // K slices whose x slice and unit slots fit in LDS.
+  // A problem whose units all fit the waves' rings at once, with all of x in LDS: the SMALL form
+  // (every load in flight from the start, no K slices).
+  if (!fused && K % 512 == 0) {
+    const int S = K >> 7;
+    const int R = ((nout + cus - 1) / cus + 3) / 4 * 4;
+    const int RB = (R + 15) / 16;
+    const int SU = S / 4;
+    const size_t xb = rowsplit_xs_bytes(K, MP);
+    const size_t pb = rowsplit_part_bytes(RB * SU, MP);
+    if (RB * SU <= kRsPF * kRsWaves && xb <= kRsLds && pb <= kRsLds &&
+        (size_t)S * 16 * MP <= (size_t)kRsSmallXP * kRsThreads) {
+      plan->MP = MP;
+      plan->small = true;
+      plan->V = 4;
+      plan->fused = false;
+      plan->Nout = nout;
+      plan->R = R;
+      plan->RB = RB;
+      plan->SU = SU;
+      plan->KS = 1;
+      plan->Kp = K;
+      plan->ranges = (nout + R - 1) / R;
+      plan->blocks = plan->ranges;
+      plan->part_bytes = 0;
+      plan->smem = std::max(xb, pb);
+      return true;
+    }
+  }
+  const int max_ks = MP == 4 ? 4 : 8;
+  for (int ks = 1; ks <= max_ks; ks *= 2) {
     if (K % (128 * ks) != 0) continue;
     const int kp = K / ks;
     const int S = kp >> 7;
@@ -366,10 +490,12 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
     const int R = ((nout + target - 1) / target + 3) / 4 * 4;
     const int RB = ((fused ? 2 * R : R) + 15) / 16;
     const int SU = S / V;
-    if (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves) continue;
-    const size_t smem = rowsplit_xs_bytes(kp) + rowsplit_part_bytes(RB * SU) + 32;
+    if (MP == 4 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
+    const size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
     if (smem > 160 * 1024) continue;
     const int ranges = (nout + R - 1) / R;
+    plan->MP = MP;
+    plan->small = false;
     plan->V = V;
     plan->fused = fused;
     plan->Nout = nout;
@@ -380,43 +506,55 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
     plan->Kp = kp;
     plan->ranges = ranges;
     plan->blocks = ranges * ks;
-    plan->part_bytes = ks > 1 ? (size_t)plan->blocks * (fused ? 2 * R : R) * 16 : 0;
+    plan->part_bytes = ks > 1 ? (size_t)plan->blocks * (fused ? 2 * R : R) * (MP / 4) * 16 : 0;
     plan->smem = smem;
     return true;
   }
   return false;
 }
 
-template <int V, bool FUSED, bool KSPLIT>
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL = false>
 hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rowsplit_kernel<V, FUSED, KSPLIT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, 160 * 1024);
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRsLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((rowsplit_kernel<V, FUSED, KSPLIT>), dim3(plan.blocks), dim3(kRsThreads), plan.smem, stream, P);
+  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL>), dim3(plan.blocks), dim3(kRsThreads), plan.smem,
+                     stream, P);
   return hipGetLastError();
 }
 
-template <int V, bool FUSED>
+template <int MP, int V, bool FUSED>
 hipError_t launch_rowsplit_k(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
-  return plan.KS > 1 ? launch_rowsplit_t<V, FUSED, true>(plan, P, stream)
-                     : launch_rowsplit_t<V, FUSED, false>(plan, P, stream);
+  return plan.KS > 1 ? launch_rowsplit_t<MP, V, FUSED, true>(plan, P, stream)
+                     : launch_rowsplit_t<MP, V, FUSED, false>(plan, P, stream);
+}
+
+template <int MP>
+hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
+  if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true>(plan, P, stream);
+  if (plan.fused)
+    return plan.V == 5 ? launch_rowsplit_k<MP, 5, true>(plan, P, stream) : launch_rowsplit_k<MP, 4, true>(plan, P, stream);
+  return plan.V == 5 ? launch_rowsplit_k<MP, 5, false>(plan, P, stream) : launch_rowsplit_k<MP, 4, false>(plan, P, stream);
 }
 
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
                            hipStream_t stream) {
+  if (M > plan.MP) return hipErrorInvalidValue;
   RowSplitParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
   P.Nout = plan.Nout; P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
   P.KS = plan.KS; P.Kp = plan.Kp; P.part = part; P.cnt = cnt;
-  if (plan.fused)
-    return plan.V == 5 ? launch_rowsplit_k<5, true>(plan, P, stream) : launch_rowsplit_k<4, true>(plan, P, stream);
-  return plan.V == 5 ? launch_rowsplit_k<5, false>(plan, P, stream) : launch_rowsplit_k<4, false>(plan, P, stream);
+  switch (plan.MP) {
+    case 4: return launch_rowsplit_m<4>(plan, P, stream);
+    case 8: return launch_rowsplit_m<8>(plan, P, stream);
+    default: return hipErrorInvalidValue;
+  }
 }
 
 }  // namespace qmm4

@@ -330,6 +330,59 @@ def test_rowsplit_one_hot_is_exact_dequant(kind):
         assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
 
 
+# Small problems (every unit in a wave's ring from the start, all of x in LDS) take the row-split
+# kernel's SMALL form: 1-8 rows over N = 1024 (4 live rows per 16-row block), 5120 (20 rows per
+# workgroup) and 4112 (a partial last range), K = 5120 (x of 8 rows is 80 KB of LDS) and 2048.
+@pytest.mark.parametrize("m,k,n", [(1, 5120, 1024), (4, 5120, 5120), (5, 5120, 5120), (8, 5120, 5120),
+                                   (7, 2048, 4112), (2, 8192, 2048)])
+def test_rowsplit_small_shapes(m, k, n):
+    note(f"row-split small {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 11 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split small {m}x{k}x{n}", (x, w, s, b))
+    assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
+# 5 to 8 rows: x rows in two lane groups of the MFMA, whole K (N = 34848 leaves a partial last
+# range), the small form with x filling all 160 KB of LDS (6 x 10240 over N = 4096), and K in two
+# slices (8 x 10240 over N = 5168: 30 units per workgroup over a whole-K x that does not fit).
+@pytest.mark.parametrize("m,k,n", [(5, 5120, 34848), (8, 4096, 34816), (6, 10240, 4096), (8, 10240, 5168)])
+def test_rowsplit_eight_row_shapes(m, k, n):
+    note(f"row-split 8-row {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 17 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split 8-row {m}x{k}x{n}", (x, w, s, b))
+    for _ in range(2):
+        assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
+@pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
+@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848)])
+def test_rowsplit_small_and_eight_row_one_hot_is_exact_dequant(kind, m, n):
+    """One-hot rows of x through the small form and the 8-row fragments: each output is one
+    dequantized weight, equal to the oracle's bit for bit (fast form, general form, both)."""
+    k = 5120
+    rng = np.random.default_rng({"fast": 31, "mixed": 32, "slow": 33}[kind] + n + m)
+    s, b = scale_bias_pairs(kind, n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in (0, 2555, 5120 - m):
+        ks = k0 + np.arange(m)
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), ks] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.empty((m, n), dtype=np.uint16)
+        for i, kk in enumerate(ks):
+            g = kk // 64
+            ref[i] = O.dequantize(w[:, 8 * g:8 * g + 8], s[:, g:g + 1], b[:, g:g + 1])[:, kk - 64 * g]
+        keep = (ref & 0x7F80) != 0  # subnormal bf16 weights test the MFMA, not the dequant
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 # ----------------------------------------------------------------------------- row-phase path
 # More than 16 rows (or up to 16 when N gives every wave its own blocks) take the row-phase kernel
 # (K a multiple of 512). Wide shapes give each workgroup whole rows over all of K (N = 16 * 2049
