@@ -9,6 +9,7 @@
 #include <hip/hip_runtime.h>
 
 #include <algorithm>
+#include <cstdint>
 #include <cstdarg>
 #include <cstdio>
 #include <map>
@@ -182,6 +183,8 @@ class StreamWorkspace final : public qmm4::WorkspaceSource {
     return QMM4_OK;
   }
 
+  size_t capacity() const override { return SIZE_MAX; }
+
   int get_scratch(size_t bytes, void** out) override {
     int rc = grow(sb_.scratch, bytes, false, 0, stream_, "gate+up scratch");
     if (rc) return rc;
@@ -334,7 +337,15 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
   int rc;
 
   if (M > 64) {
-    e = launch_gemm(xb, w, sb, bb, yb, (int)M, (int)N, (int)K, di->cus, stream);
+    GemmPlan gplan;
+    gemm_plan((int)M, (int)N, (int)K, di->cus, ws.capacity(), sb, bb, &gplan);
+    uint32_t* gcnt = nullptr;
+    float* gpart = nullptr;
+    if (gplan.sk) {
+      rc = ws.get(0, gplan.part_bytes, &gcnt, &gpart);
+      if (rc) return rc;
+    }
+    e = launch_gemm(gplan, xb, w, sb, bb, yb, gpart, (int)M, (int)N, (int)K, di->cus, stream);
     if (e != hipSuccess) return hip_error(e, "gemm kernel launch");
     return QMM4_OK;
   }

@@ -28,6 +28,8 @@ int device_cus(const DeviceInfo* di);
 class WorkspaceSource {
  public:
   virtual int get(size_t counter_bytes, size_t partial_bytes, uint32_t** cnt, float** part) = 0;
+  // The most partial bytes get() can provide.
+  virtual size_t capacity() const = 0;
   // Scratch for the [M, N] projection of the two-pass gate+up epilogue.
   virtual int get_scratch(size_t bytes, void** out) = 0;
 

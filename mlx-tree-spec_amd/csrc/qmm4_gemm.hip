@@ -44,10 +44,27 @@ struct GemmParams {
   const uint16_t* b;
   uint16_t* y;
   int M, N, K;
-  int tiles_m, tiles_n;  // 256 x 256 tiles
+  int tiles_m, tiles_n;  // tiles of the grid (256 x 256, or BM x BN for a stream-K launch)
   int tile0;             // first tile (in walk order) of this launch
-  int quarter;           // 1: each workgroup computes one 128 x 128 quarter of a tile
+  int quarter;           // 1: each workgroup computes one 128 x 128 quarter of a 256 x 256 tile
+  // Stream-K (sk = 1): the tiles x K units (ups K steps each) are split into G contiguous
+  // ranges, one per workgroup; a workgroup runs its range tile segment by tile segment. A segment
+  // covering a whole tile writes bf16 y; a workgroup's first and last segments may cover part of
+  // a tile and then leave fp32 partial tiles in part[(workgroup * 2 + slot) * BM * BN] (slot 0:
+  // first segment, 1: last), which the reduce kernel adds in K order.
+  int sk;
+  int upt;           // K units per tile
+  int ups;           // K steps (BK) per unit
+  long long U;       // tiles * upt
+  float* part;
 };
+
+// Stream-K range of workgroup p: units [p U / G, (p + 1) U / G).
+__host__ __device__ inline long long sk_start(int p, long long U, int G) { return (long long)p * U / G; }
+// The workgroup whose range holds unit u.
+__host__ __device__ inline int sk_owner(long long u, long long U, int G) {
+  return (int)(((u + 1) * (long long)G + U - 1) / U) - 1;
+}
 
 template <int BM, int BN>
 struct GemmCfg {
@@ -60,6 +77,7 @@ struct GemmCfg {
   static constexpr int WV = (WPT + 3) / 4;              // 16-byte word vectors per thread
   static constexpr int LDC = BN + 8;                    // LDS row pitch (bf16) of the output tile
   static constexpr size_t kSmem = (size_t)2 * (BM + BN) * LDK * sizeof(uint16_t);
+  static constexpr int kPartF4 = BM * BN / 4;           // f32x4 items of a partial tile
   static_assert((size_t)BM * LDC * sizeof(uint16_t) <= kSmem, "output tile fits the K-step stages");
   static_assert(I >= 1 && J >= 1 && (WPT == 2 || WPT == 4 || WPT == 8) && AJ % 2 == 0, "tile shape");
 };
@@ -72,10 +90,29 @@ struct Raw {
   uint32_t s, b;      // that group's scale and bias (bf16 bits)
 };
 
+// Partial-tile item e (f32x4) of a wave's accumulators: item ((((wave * I + i) * J + j) * 4 + rq)
+// * 64 + lane) holds acc[i][j][4 rq .. 4 rq + 3] of that lane.
+template <class C>
+__device__ __forceinline__ void part_item_coords(int e, int* m, int* n) {
+  const int lane = e & 63;
+  int rest = e >> 6;
+  const int rq = rest & 3;
+  rest >>= 2;
+  const int j = rest % C::J;
+  rest /= C::J;
+  const int i = rest % C::I;
+  const int wave = rest / C::I;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;
+  *m = wm * C::WM + i * 32 + 8 * rq + 4 * (lane >> 5);  // rows m .. m + 3 of the item's four values
+  *n = wn * C::WN + j * 32 + (lane & 31);
+}
+
 // SB8: scales and biases are loaded 8 groups (8 K steps) at a time with one 16-byte load per
 // column (K % 512 == 0); otherwise one 2-byte load per K step.
+// The 128 x 128 configuration is held to 128 VGPRs so that two workgroups share a CU.
 template <int BM, int BN, bool SB8>
-__global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 128 ? 4 : 2)))
+void gemm_kernel(GemmParams P) {
   using C = GemmCfg<BM, BN>;
   constexpr int I = C::I, J = C::J, AJ = C::AJ, WPT = C::WPT, LDC = C::LDC;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -86,9 +123,11 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int wm = wave / kWavesN, wn = wave % kWavesN;
+  const int nk = P.K / BK;  // even: K % 128 == 0
 
-  // Tile: XCD-contiguous remap of full-tile launches, then a grouped row-major walk of the
-  // 256 x 256 tiles; a quarter launch gives each tile's four 128 x 128 quarters to four workgroups.
+  // Workgroup order: an XCD-contiguous remap (consecutive walk positions on one XCD) for
+  // full-tile and stream-K launches; a quarter launch gives each tile's four 128 x 128 quarters
+  // to four consecutive workgroups.
   const int G = gridDim.x;
   int bid = blockIdx.x;
   int q = 0;
@@ -98,16 +137,18 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
   } else if ((G & 7) == 0) {
     bid = (bid & 7) * (G >> 3) + (bid >> 3);
   }
-  const int id = P.tile0 + bid;
-  const int per_group = kGroupM * P.tiles_n;
-  const int group = id / per_group;
-  const int first_m = group * kGroupM;
-  const int gm = min(kGroupM, P.tiles_m - first_m);
-  const int in_group = id - group * per_group;
-  const int tm = first_m + in_group % gm;
-  const int tn = in_group / gm;
-  const int m0 = tm * kTile + (q >> 1) * BM, n0 = tn * kTile + (q & 1) * BN;
-  const int nk = P.K / BK;  // even: K % 128 == 0
+  // Tile id -> first row and column: a grouped row-major walk (kGroupM row tiles at a time, so a
+  // group shares weight and activation blocks in L2).
+  const int tile_rows = P.sk ? BM : kTile, tile_cols = P.sk ? BN : kTile;
+  auto tile_origin = [&](int id, int* m0, int* n0) __attribute__((always_inline)) {
+    const int per_group = kGroupM * P.tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * kGroupM;
+    const int gm = min(kGroupM, P.tiles_m - first_m);
+    const int in_group = id - group * per_group;
+    *m0 = (first_m + in_group % gm) * tile_rows + (q >> 1) * BM;
+    *n0 = (in_group / gm) * tile_cols + (q & 1) * BN;
+  };
 
   const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
@@ -117,189 +158,284 @@ __global__ __launch_bounds__(kThreads) void gemm_kernel(GemmParams P) {
       const_cast<uint16_t*>(P.s), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
   const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
       const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
 
   // Loader roles. Activations: 16-byte chunk a_kc of rows a_r0 + 64 j (row j's offset goes in the
   // scalar offset). Weights: words WPT * b_part .. + WPT - 1 of column n0 + b_col.
   const int a_kc = tid & 7;
   const int a_r0 = tid >> 3;
-  const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
   const int xrowp = C::RPP * P.K * 2;  // byte distance of consecutive load passes
   const int b_col = tid / C::TPC, b_part = tid % C::TPC;
-  const uint32_t col = (uint32_t)(n0 + b_col);
-  const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)(b_part * WPT * 4);
-  const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
-
-  Raw<C> raw[2];
-  // Steps past the last are clamped to it (their data is written to an LDS stage nobody reads).
-  auto load = [&](int kt, Raw<C>& R) {
-    const int k = kt < nk ? kt : nk - 1;
-#pragma unroll
-    for (int j = 0; j < AJ; ++j)
-      R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrowp, 0);
-    if constexpr (WPT >= 4) {
-#pragma unroll
-      for (int v = 0; v < C::WV; ++v) R.w[v] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff + v * 16, k * 32, 0);
-    } else {
-      const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rw, woff, k * 32, 0);
-      R.w[0] = u32x4{t.x, t.y, 0u, 0u};
-    }
-    if constexpr (!SB8) {
-      R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
-      R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
-    }
-  };
-  // SB8: groups 8 q .. 8 q + 7 of this thread's column; scur holds the block of the step being
-  // written to LDS, snext the following block (loaded 3 steps before it is first needed).
-  u32x4 scur = {0u, 0u, 0u, 0u}, bcur = scur, snext = scur, bnext = scur;
-  auto load_sb8 = [&](int kt, u32x4& s8, u32x4& b8) __attribute__((always_inline)) {
-    const int k = kt < nk ? kt : 0;
-    s8 = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 2, 0);
-    b8 = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 2, 0);
-  };
-  // Group kt % 8 of a block: dword (kt % 8) / 2, half kt % 2 (wave-uniform selects).
-  auto pick = [&](const u32x4& v, int kt) __attribute__((always_inline)) {
-    const int d = (kt >> 1) & 3;
-    const uint32_t w = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
-    return (kt & 1) ? (w >> 16) : (w & 0xFFFFu);
-  };
-  // Scale and bias bits of step kt for the weight stores.
-  auto sb_of = [&](const Raw<C>& R, int kt, uint32_t& sb, uint32_t& bb) __attribute__((always_inline)) {
-    if constexpr (SB8) {
-      sb = pick(scur, kt);
-      bb = pick(bcur, kt);
-    } else {
-      sb = R.s & 0xFFFFu;
-      bb = R.b & 0xFFFFu;
-    }
-  };
-  auto store_a = [&](const Raw<C>& R, int st, int j0, int j1) {
-    uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
-#pragma unroll
-    for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + C::RPP * j * LDK) = R.a[j];
-  };
-  auto store_b_fast = [&](const Raw<C>& R, int st, int j0, int j1, uint32_t sbits, uint32_t bbits) {
-    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
-    const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
-    const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
-#pragma unroll
-    for (int j = j0; j < j1; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j >> 2][j & 3], s24, s20, bf);
-  };
-  auto store_b_exact = [&](const Raw<C>& R, int st, uint32_t sbits, uint32_t bbits) {
-    uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
-    const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
-#pragma unroll
-    for (int j = 0; j < WPT; ++j)
-      *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
-  };
-
-  f32x16 acc[I][J];
-#pragma unroll
-  for (int i = 0; i < I; ++i)
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
-
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * 8;
 
-  // Step kt: MFMAs from LDS stage kt % 2 while step kt + 1 (raw[(kt + 1) % 2]) is written into the
-  // other stage; then step kt + 3 is loaded into the registers just written out.
-  auto step = [&](int kt, auto parity) {
-    constexpr int ST = decltype(parity)::value;
-    Raw<C>& R = raw[ST ^ 1];
-    if constexpr (SB8) {
-      // Step kt + 1 starts a block of 8 groups: move to it.
-      if (((kt + 1) & 7) == 0) {
-        scur = snext;
-        bcur = bnext;
-      }
-    }
-    uint32_t sbits, bbits;
-    sb_of(R, kt + 1, sbits, bbits);
-    const uint16_t* as = As + ST * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
-    const uint16_t* bs = Bs + ST * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
-    // Fragments are double-buffered across the four 16-k sub-steps: sub-step ks + 1's reads are
-    // issued before sub-step ks's MFMAs, so LDS latency hides behind them.
-    bf16x8 Af[2][I], Bf[2][J];
-    auto frags = [&](int ks, int sl) __attribute__((always_inline)) {
+  f32x16 acc[I][J];
+
+  // One tile segment: K steps [kb, ke) of the tile at (m0, n0) into acc (kb and ke even; with
+  // SB8 multiples of 8).
+  auto run_segment = [&](int m0, int n0, int kb, int ke) __attribute__((always_inline)) {
+    const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
+    const uint32_t col = (uint32_t)(n0 + b_col);
+    const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)(b_part * WPT * 4);
+    const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
+
+    Raw<C> raw[2];
+    // Steps past the segment's last are clamped to it (their data is written to an LDS stage
+    // nobody reads).
+    auto load = [&](int kt, Raw<C>& R) {
+      const int k = kt < ke ? kt : ke - 1;
 #pragma unroll
-      for (int i = 0; i < I; ++i)
-        Af[sl][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
+      for (int j = 0; j < AJ; ++j)
+        R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrowp, 0);
+      if constexpr (WPT >= 4) {
+#pragma unroll
+        for (int v = 0; v < C::WV; ++v) R.w[v] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff + v * 16, k * 32, 0);
+      } else {
+        const u32x2 t = __builtin_amdgcn_raw_buffer_load_b64(rw, woff, k * 32, 0);
+        R.w[0] = u32x4{t.x, t.y, 0u, 0u};
+      }
+      if constexpr (!SB8) {
+        R.s = __builtin_amdgcn_raw_buffer_load_b16(rs, soff, k * 2, 0);
+        R.b = __builtin_amdgcn_raw_buffer_load_b16(rb, soff, k * 2, 0);
+      }
+    };
+    // SB8: groups 8 q .. 8 q + 7 of this thread's column; scur holds the block of the step being
+    // written to LDS, snext the following block (loaded 3 steps before it is first needed).
+    u32x4 scur = {0u, 0u, 0u, 0u}, bcur = scur, snext = scur, bnext = scur;
+    auto load_sb8 = [&](int kt, u32x4& s8, u32x4& b8) __attribute__((always_inline)) {
+      const int k = kt < ke ? kt : kb;
+      s8 = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 2, 0);
+      b8 = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 2, 0);
+    };
+    // Group kt % 8 of a block: dword (kt % 8) / 2, half kt % 2 (wave-uniform selects).
+    auto pick = [&](const u32x4& v, int kt) __attribute__((always_inline)) {
+      const int d = (kt >> 1) & 3;
+      const uint32_t w = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
+      return (kt & 1) ? (w >> 16) : (w & 0xFFFFu);
+    };
+    // Scale and bias bits of step kt for the weight stores.
+    auto sb_of = [&](const Raw<C>& R, int kt, uint32_t& sb, uint32_t& bb) __attribute__((always_inline)) {
+      if constexpr (SB8) {
+        sb = pick(scur, kt);
+        bb = pick(bcur, kt);
+      } else {
+        sb = R.s & 0xFFFFu;
+        bb = R.b & 0xFFFFu;
+      }
+    };
+    auto store_a = [&](const Raw<C>& R, int st, int j0, int j1) {
+      uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
+#pragma unroll
+      for (int j = j0; j < j1; ++j) *reinterpret_cast<u32x4*>(as + C::RPP * j * LDK) = R.a[j];
+    };
+    auto store_b_fast = [&](const Raw<C>& R, int st, int j0, int j1, uint32_t sbits, uint32_t bbits) {
+      uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
+      const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
+      const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
+#pragma unroll
+      for (int j = j0; j < j1; ++j)
+        *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j >> 2][j & 3], s24, s20, bf);
+    };
+    auto store_b_exact = [&](const Raw<C>& R, int st, uint32_t sbits, uint32_t bbits) {
+      uint16_t* bs = Bs + st * BN * LDK + b_col * LDK + b_part * WPT * 8;
+      const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
+#pragma unroll
+      for (int j = 0; j < WPT; ++j)
+        *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
+    };
+
+#pragma unroll
+    for (int i = 0; i < I; ++i)
 #pragma unroll
       for (int j = 0; j < J; ++j)
-        Bf[sl][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
-    };
-    frags(0, 0);
 #pragma unroll
-    for (int ks = 0; ks < BK / 16; ++ks) {
-      if (ks + 1 < BK / 16) frags(ks + 1, (ks + 1) & 1);
+        for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+    // Step kt: MFMAs from LDS stage kt % 2 while step kt + 1 (raw[(kt + 1) % 2]) is written into
+    // the other stage; then step kt + 3 is loaded into the registers just written out.
+    auto step = [&](int kt, auto parity) {
+      constexpr int ST = decltype(parity)::value;
+      Raw<C>& R = raw[ST ^ 1];
+      if constexpr (SB8) {
+        // Step kt + 1 starts a block of 8 groups: move to it.
+        if (((kt + 1) & 7) == 0) {
+          scur = snext;
+          bcur = bnext;
+        }
+      }
+      uint32_t sbits, bbits;
+      sb_of(R, kt + 1, sbits, bbits);
+      const uint16_t* as = As + ST * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
+      const uint16_t* bs = Bs + ST * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
+      // Fragments are double-buffered across the four 16-k sub-steps: sub-step ks + 1's reads are
+      // issued before sub-step ks's MFMAs, so LDS latency hides behind them.
+      bf16x8 Af[2][I], Bf[2][J];
+      auto frags = [&](int ks, int sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+          Af[sl][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          Bf[sl][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
+      };
+      frags(0, 0);
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        if (ks + 1 < BK / 16) frags(ks + 1, (ks + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+#pragma unroll
+          for (int j = 0; j < J; ++j) acc[i][j] = Mfma<32>::mma(Af[ks & 1][i], Bf[ks & 1][j], acc[i][j]);
+        if (ks == 0) store_a(R, ST ^ 1, 0, AJ / 2);
+        if (ks == 1) store_a(R, ST ^ 1, AJ / 2, AJ);
+        if (ks == 2) store_b_fast(R, ST ^ 1, 0, WPT / 2, sbits, bbits);
+        if (ks == 3) store_b_fast(R, ST ^ 1, WPT / 2, WPT, sbits, bbits);
+      }
+      if (!fast_scale_ok(sbits)) store_b_exact(R, ST ^ 1, sbits, bbits);
+      __syncthreads();
+      load(kt + 3, R);
+      if constexpr (SB8)
+        if (((kt + 3) & 7) == 0) load_sb8(kt + 3, snext, bnext);
+      // Keep these loads right behind the barrier (the scheduler would sink them toward their use
+      // two steps later, into the middle of the next step's MFMAs).
+      __builtin_amdgcn_sched_barrier(0);
+    };
+
+    // Prologue: steps kb and kb + 1 in registers, step kb in LDS, step kb + 2 in flight.
+    load(kb, raw[0]);
+    load(kb + 1, raw[1]);
+    if constexpr (SB8) load_sb8(kb, scur, bcur);
+    {
+      uint32_t sbits, bbits;
+      sb_of(raw[0], kb, sbits, bbits);
+      store_a(raw[0], 0, 0, AJ);
+      store_b_fast(raw[0], 0, 0, WPT, sbits, bbits);
+      if (!fast_scale_ok(sbits)) store_b_exact(raw[0], 0, sbits, bbits);
+    }
+    load(kb + 2, raw[0]);
+    __syncthreads();
+
+    for (int kt = kb; kt < ke; kt += 2) {
+      step(kt, std::integral_constant<int, 0>{});
+      step(kt + 1, std::integral_constant<int, 1>{});
+    }
+  };
+
+  // The tile as bf16 through LDS (every wave is past the last step's reads), then 16-byte row
+  // chunks; rows past M fall outside y's buffer resource, columns past N are skipped (N % 16 == 0,
+  // so a chunk is entirely inside or outside).
+  auto write_tile = [&](int m0, int n0) __attribute__((always_inline)) {
+    uint16_t* Cs = smem;
+#pragma unroll
+    for (int i = 0; i < I; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int n = wn * C::WN + j * 32 + lrow;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = wm * C::WM + i * 32 + Mfma<32>::row(lane, r);
+          Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
+        }
+      }
+    __syncthreads();
+    constexpr int kChunksPerRow = BN / 8;
+#pragma unroll 4
+    for (int c = tid; c < BM * kChunksPerRow; c += kThreads) {
+      const int r = c / kChunksPerRow, ch = c % kChunksPerRow;
+      const int gn = n0 + ch * 8;
+      if (gn < P.N) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)(m0 + r) * (uint32_t)P.N + (uint32_t)gn) * 2u, 0, 0);
+      }
+    }
+  };
+
+  if (!P.sk) {
+    int m0, n0;
+    tile_origin(P.tile0 + bid, &m0, &n0);
+    run_segment(m0, n0, 0, nk);
+    write_tile(m0, n0);
+    return;
+  }
+
+  // Stream-K: this workgroup's units, tile segment by tile segment.
+  const long long u0 = sk_start(bid, P.U, G), u1 = sk_start(bid + 1, P.U, G);
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      P.part, 0, rsrc_bytes((unsigned long long)G * 2 * C::kPartF4 * 16), kBufferRsrcWord3);
+  for (long long u = u0; u < u1;) {
+    const int t = (int)(u / P.upt);
+    const long long tb = (long long)t * P.upt;
+    const long long e = u1 < tb + P.upt ? u1 : tb + P.upt;
+    const int kb = (int)(u - tb) * P.ups, ke = (int)(e - tb) * P.ups;
+    int m0, n0;
+    tile_origin(t, &m0, &n0);
+    run_segment(m0, n0, kb, ke);
+    if (kb == 0 && ke == nk) {
+      write_tile(m0, n0);
+    } else {
+      // A part of the tile: its fp32 sums to this workgroup's slot (0: its first segment, 1: its
+      // last), item-major per lane (16-byte stores).
+      const uint32_t slot = (uint32_t)bid * 2u + (u == u0 ? 0u : 1u);
 #pragma unroll
       for (int i = 0; i < I; ++i)
 #pragma unroll
-        for (int j = 0; j < J; ++j) acc[i][j] = Mfma<32>::mma(Af[ks & 1][i], Bf[ks & 1][j], acc[i][j]);
-      if (ks == 0) store_a(R, ST ^ 1, 0, AJ / 2);
-      if (ks == 1) store_a(R, ST ^ 1, AJ / 2, AJ);
-      if (ks == 2) store_b_fast(R, ST ^ 1, 0, WPT / 2, sbits, bbits);
-      if (ks == 3) store_b_fast(R, ST ^ 1, WPT / 2, WPT, sbits, bbits);
+        for (int j = 0; j < J; ++j)
+#pragma unroll
+          for (int rq = 0; rq < 4; ++rq) {
+            const uint32_t item = (uint32_t)((((wave * I + i) * J + j) * 4 + rq) * 64 + lane);
+            const f32x4 v = {acc[i][j][4 * rq], acc[i][j][4 * rq + 1], acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]};
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
+                                                   (slot * (uint32_t)C::kPartF4 + item) * 16u, 0, 0);
+          }
     }
-    if (!fast_scale_ok(sbits)) store_b_exact(R, ST ^ 1, sbits, bbits);
-    __syncthreads();
-    load(kt + 3, R);
-    if constexpr (SB8)
-      if (((kt + 3) & 7) == 0) load_sb8(kt + 3, snext, bnext);
-    // Keep these loads right behind the barrier (the scheduler would sink them toward their use two
-    // steps later, into the middle of the next step's MFMAs).
-    __builtin_amdgcn_sched_barrier(0);
-  };
-
-  // Prologue: steps 0 and 1 in registers, step 0 in LDS, step 2 in flight.
-  load(0, raw[0]);
-  load(1, raw[1]);
-  if constexpr (SB8) load_sb8(0, scur, bcur);
-  {
-    uint32_t sbits, bbits;
-    sb_of(raw[0], 0, sbits, bbits);
-    store_a(raw[0], 0, 0, AJ);
-    store_b_fast(raw[0], 0, 0, WPT, sbits, bbits);
-    if (!fast_scale_ok(sbits)) store_b_exact(raw[0], 0, sbits, bbits);
+    u = e;
+    __syncthreads();  // the next segment's prologue reuses the LDS stages (and the output tile)
   }
-  load(2, raw[0]);
-  __syncthreads();
+}
 
-  for (int kt = 0; kt < nk; kt += 2) {
-    step(kt, std::integral_constant<int, 0>{});
-    step(kt + 1, std::integral_constant<int, 1>{});
+// Stream-K fix-up: the tiles split between workgroups, their partial sums added in K order (the
+// owners of a tile's units in increasing order; a tile is the last segment of its first owner
+// when that owner's range began in an earlier tile), one f32x4 item per thread, bf16 y.
+constexpr int kSkRedThreads = 256;
+template <int BM, int BN>
+__global__ __launch_bounds__(kSkRedThreads) void gemm_sk_reduce_kernel(GemmParams P, int G) {
+  using C = GemmCfg<BM, BN>;
+  const long long it = (long long)blockIdx.x * kSkRedThreads + threadIdx.x;
+  const int t = (int)(it / C::kPartF4);
+  const int e = (int)(it - (long long)t * C::kPartF4);
+  if (t >= P.tiles_m * P.tiles_n) return;
+  const long long tb = (long long)t * P.upt;
+  const int lo = sk_owner(tb, P.U, G), hi = sk_owner(tb + P.upt - 1, P.U, G);
+  if (lo == hi) return;  // one workgroup ran the whole tile and wrote it
+  const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+      P.part, 0, rsrc_bytes((unsigned long long)G * 2 * C::kPartF4 * 16), kBufferRsrcWord3);
+  f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+  for (int c = lo; c <= hi; ++c) {
+    const uint32_t slot = (uint32_t)c * 2u + ((c == lo && sk_start(lo, P.U, G) < tb) ? 1u : 0u);
+    const f32x4 v = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(
+                                                  rp, (slot * (uint32_t)C::kPartF4 + (uint32_t)e) * 16u, 0, 0));
+    sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
   }
-
-  // Epilogue: the tile as bf16 through LDS (every wave is past the last step's reads), then
-  // 16-byte row chunks; rows past M fall outside y's buffer resource, columns past N are skipped
-  // (N % 16 == 0, so a chunk is entirely inside or outside).
-  uint16_t* Cs = smem;
-#pragma unroll
-  for (int i = 0; i < I; ++i)
-#pragma unroll
-    for (int j = 0; j < J; ++j) {
-      const int n = wn * C::WN + j * 32 + lrow;
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const int m = wm * C::WM + i * 32 + Mfma<32>::row(lane, r);
-        Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
-      }
-    }
-  __syncthreads();
+  // Tile origin (the same grouped walk as the main kernel).
+  const int per_group = kGroupM * P.tiles_n;
+  const int group = t / per_group;
+  const int first_m = group * kGroupM;
+  const int gm = min(kGroupM, P.tiles_m - first_m);
+  const int in_group = t - group * per_group;
+  const int m0 = (first_m + in_group % gm) * BM, n0 = (in_group / gm) * BN;
+  int mi, ni;
+  part_item_coords<C>(e, &mi, &ni);
+  const int n = n0 + ni;
+  if (n >= P.N) return;
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
       P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
-  constexpr int kChunksPerRow = BN / 8;
-#pragma unroll 4
-  for (int c = tid; c < BM * kChunksPerRow; c += kThreads) {
-    const int r = c / kChunksPerRow, ch = c % kChunksPerRow;
-    const int gn = n0 + ch * 8;
-    if (gn < P.N) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
-      __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)(m0 + r) * (uint32_t)P.N + (uint32_t)gn) * 2u, 0, 0);
-    }
+#pragma unroll
+  for (int r = 0; r < 4; ++r) {
+    const int m = m0 + mi + r;
+    if (m < P.M)
+      __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16x2(sum[r], 0.0f) & 0xFFFFu), ry,
+                                            ((uint32_t)m * (uint32_t)P.N + (uint32_t)n) * 2u, 0, 0);
   }
 }
 
@@ -317,16 +453,88 @@ hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
   return hipGetLastError();
 }
 
+template <int BM, int BN>
+hipError_t launch_sk_reduce(const GemmParams& P, int G, hipStream_t stream) {
+  const long long items = (long long)P.tiles_m * P.tiles_n * GemmCfg<BM, BN>::kPartF4;
+  hipLaunchKernelGGL((gemm_sk_reduce_kernel<BM, BN>), dim3((unsigned)((items + kSkRedThreads - 1) / kSkRedThreads)),
+                     dim3(kSkRedThreads), 0, stream, P, G);
+  return hipGetLastError();
+}
+
+// Resident stream-K workgroups per CU (the 128 x 128 configuration: 74 KB of LDS each).
+int sk_occupancy(bool sb8) {
+  static int occ[2] = {0, 0};
+  int& o = occ[sb8 ? 1 : 0];
+  if (o == 0) {
+    const void* f = sb8 ? reinterpret_cast<const void*>(&gemm_kernel<128, 128, true>)
+                        : reinterpret_cast<const void*>(&gemm_kernel<128, 128, false>);
+    constexpr size_t smem = GemmCfg<128, 128>::kSmem;
+    int nb = 0;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kThreads, smem) != hipSuccess || nb < 1)
+      nb = 1;
+    o = nb < 2 ? nb : 2;
+  }
+  return o;
+}
+
+bool scale_rows_16b(const uint16_t* s, const uint16_t* b, int K) {
+  return K % 512 == 0 && (reinterpret_cast<uintptr_t>(s) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0;
+}
+
 }  // namespace
 
-// Whole rounds of 256 x 256 tiles (one per CU at a time) in one launch; when the last round would
-// leave most CUs idle, its tiles are cut into 128 x 128 quarters and launched next, so that round
-// runs on four times as many CUs at about a third of a tile's time.
-hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* y,
-                       int M, int N, int K, int cus, hipStream_t stream) {
+// More 128 x 128 tiles than CUs: whole rounds of 256 x 256 tiles (one per CU at a time) in one
+// launch; when the last round would leave most CUs idle, its tiles are cut into 128 x 128 quarters
+// and launched next. Fewer tiles (e.g. a short prompt tail or more than 64 tree nodes over a
+// narrow output): stream-K over 128 x 128 tiles, the tiles x K units split evenly over every
+// resident workgroup slot, then the fix-up of the split tiles.
+bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t* s, const uint16_t* b, GemmPlan* plan) {
+  const int c = cus > 0 ? cus : 1;
+  plan->sk = false;
+  plan->G = 0;
+  plan->part_bytes = 0;
+  // Measured on MI355X (5120 -> 17408 and 17408 -> 5120 at 65 to 2048 rows): stream-K over
+  // 128 x 128 tiles wins while there are no more such tiles than CUs (1.9-3.2x at 65-256 rows);
+  // with more, whole 256 x 256 tiles (a 128 x 128 tile reads its LDS fragments for half as many
+  // MFMAs) are faster.
+  const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
+  if (tiles > c) return true;
+  const bool sb8 = scale_rows_16b(s, b, K);
+  const int ups = sb8 ? 8 : 2;
+  const long long U = tiles * (K / BK / ups);
+  long long G = (long long)c * sk_occupancy(sb8);
+  if (G > U) G = U;
+  const size_t slot = (size_t)GemmCfg<128, 128>::kPartF4 * 16 * 2;  // two partial tiles per workgroup
+  if ((size_t)G * slot > ws_capacity) G = (long long)(ws_capacity / slot);
+  if (G < c / 2) return true;  // too little workspace to spread the tiles: whole tiles instead
+  plan->sk = true;
+  plan->G = (int)G;
+  plan->part_bytes = (size_t)G * slot;
+  return true;
+}
+
+hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s, const uint16_t* b,
+                       uint16_t* y, float* part, int M, int N, int K, int cus, hipStream_t stream) {
   GemmParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
+  P.sk = 0; P.upt = 0; P.ups = 0; P.U = 0; P.part = part;
+  // 16-byte loads of 8 groups need 16-byte aligned scale rows and pointers.
+  const bool sb8 = scale_rows_16b(s, b, K);
+  if (plan.sk) {
+    P.tiles_m = (M + 127) / 128;
+    P.tiles_n = (N + 127) / 128;
+    P.tile0 = 0;
+    P.quarter = 0;
+    P.sk = 1;
+    P.ups = sb8 ? 8 : 2;
+    P.upt = K / BK / P.ups;
+    P.U = (long long)P.tiles_m * P.tiles_n * P.upt;
+    hipError_t e = sb8 ? launch_tiles<128, 128, true>(P, plan.G, stream) : launch_tiles<128, 128, false>(P, plan.G, stream);
+    if (e != hipSuccess) return e;
+    return launch_sk_reduce<128, 128>(P, plan.G, stream);
+  }
   P.tiles_m = (M + kTile - 1) / kTile;
   P.tiles_n = (N + kTile - 1) / kTile;
   const int total = P.tiles_m * P.tiles_n;
@@ -334,8 +542,6 @@ hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s, 
   const int rem = total % c;
   const int tail = (rem > 0 && 4 * rem <= 2 * c) ? rem : 0;
   const int main_tiles = total - tail;
-  // 16-byte loads of 8 groups need 16-byte aligned scale rows and pointers.
-  const bool sb8 = K % 512 == 0 && (reinterpret_cast<uintptr_t>(s) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0;
   if (main_tiles > 0) {
     P.tile0 = 0;
     P.quarter = 0;

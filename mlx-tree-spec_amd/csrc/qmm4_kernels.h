@@ -113,9 +113,21 @@ hipError_t launch_add_rms_norm(const uint16_t* x, const uint16_t* r, const uint1
 // Zero n uint32 words (the skinny kernel's arrival counters when their workspace is allocated).
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 
-// LDS-tiled MFMA GEMM for M > 64.
-hipError_t launch_gemm(const uint16_t* x, const uint32_t* w, const uint16_t* s,
-                       const uint16_t* b, uint16_t* y, int M, int N, int K, int cus, hipStream_t stream);
+// LDS-tiled MFMA GEMM for M > 64: whole 256 x 256 tiles when there are more 128 x 128 tiles than
+// CUs, otherwise stream-K over 128 x 128 tiles (fp32 partials of split tiles in the workspace,
+// added by a fix-up kernel behind the first).
+struct GemmPlan {
+  bool sk;            // stream-K
+  int G;              // stream-K workgroups
+  size_t part_bytes;  // stream-K partial tiles (two per workgroup)
+};
+// `ws_capacity`: the most partial-tile bytes the caller's workspace can hold (stream-K spreads
+// over fewer workgroups when it is small).
+bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t* s, const uint16_t* b,
+               GemmPlan* plan);
+hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
+                       const uint16_t* b, uint16_t* y, float* part, int M, int N, int K, int cus,
+                       hipStream_t stream);
 
 // Bit-exact dequantization to bf16 [N, K].
 hipError_t launch_dequant(const uint32_t* w, const uint16_t* s, const uint16_t* b,

@@ -78,6 +78,8 @@ class StaticWorkspace final : public WorkspaceSource {
     return QMM4_OK;
   }
 
+  size_t capacity() const override { return kNoallocBytes - kNoallocCounterBytes; }
+
   int get_scratch(size_t bytes, void**) override {
     return set_error(QMM4_ERR_INVALID, "qmm4_affine_bf16_noalloc: no scratch for %zu bytes", bytes);
   }

@@ -228,6 +228,38 @@ def workload_ref(x, w, s, b):
     return cpu.qmm_f32(x, w, s, b).astype(np.float64)
 
 
+# Mid-size M with few output tiles takes the GEMM's stream-K form: 128 x 128 tiles x K units
+# spread over every resident workgroup, tiles split between workgroups added by a fix-up kernel in
+# K order. 65 rows of the down projection (40 tiles over 17408 of K), the up projection at 128 rows,
+# K = 1152 (units of two K steps: K % 512 != 0), N = 784 and M = 200 (partial column and row tiles).
+@pytest.mark.parametrize("m,k,n", [(65, 17408, 5120), (128, 5120, 17408), (100, 1152, 4096), (200, 5120, 784),
+                                   (96, 512, 1024)])
+def test_gemm_stream_k_shapes(m, k, n):
+    note(f"stream-K {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=m * 19 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"stream-K {m}x{k}x{n}", (x, w, s, b))
+    for _ in range(2):  # the same split points and fix-up order every call
+        assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
+def test_gemm_stream_k_unaligned_scales():
+    """Scale and bias rows that are not 16-byte aligned: per-step scale loads and 2-step units."""
+    m, k, n = 130, 1024, 512
+    x, w, s, b = O.make_inputs(m, k, n, seed=77)
+    pad = lambda a: bf16_dev(np.concatenate([np.zeros(2, np.uint16), a.reshape(-1)]))[2:].view(n, k // 64)
+    sd, bd = pad(s), pad(b)
+    assert sd.data_ptr() % 16 == 4
+    from mlx_tree_spec_amd import _lib
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
+    xd, wd = bf16_dev(x), u32_dev(w)
+    rc = _lib.load().qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), y.data_ptr(),
+                                      m, n, k, 64, 4, 1, torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, _lib.last_error()
+    check_qmm(host_bits(y), O.quantized_matmul_exact(x, w, s, b), "stream-K unaligned scales", (x, w, s, b))
+
+
 @pytest.mark.parametrize("index,m", [(0, 16), (1, 1), (1, 2), (1, 4), (2, 64), (3, 32)])
 def test_workload_full(index, m):
     note(f"workload {index} M={m}")
