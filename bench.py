@@ -47,6 +47,17 @@ WORKLOADS = {
     "c3": (3, (32,), 5120, 151936, 1.0),
     "c4": (4, (4096,), 5120, 17408, 1.0),
 }
+# Mid-size M (a short prompt tail, more than 64 tree nodes): the model's up and down projections at
+# 65 to 2048 rows. name: (seed, rows, K, N, sigma)
+MID = {
+    "up": (6, (65, 128, 256, 512, 1024, 2048), 5120, 17408, 1.0),
+    "down": (7, (65, 128, 256, 512, 1024, 2048), 17408, 5120, 0.5),
+}
+# The dominant kernel of the headline workload and the committed rocprofv3 summaries the roofline
+# record reads (the traffic figure is used only if its summary names this kernel).
+HEAD_KERNEL = "rowsplit_kernel<4, 4, false, false, false>"
+TRACE_PROFILE = "qmm4_bench_workloads_kernel_trace.txt"
+TRAFFIC_PROFILE = "rowsplit_decode_gate_up_traffic.txt"
 DESCR = {
     "c0": "tree-verify qmm: x bf16 [16, 5120] @ packed 4-bit [5120, 5120]",
     "c1": "decode gate+up: x bf16 [M=1,2,4, 5120] @ packed 4-bit [34816, 5120]",
@@ -67,10 +78,10 @@ def bytes_per_call(m: int, k: int, n: int) -> int:
 class Workload:
     """Device-resident inputs of one benchmark workload with rotating weight copies."""
 
-    def __init__(self, name: str, torch, lib, dev):
+    def __init__(self, name: str, torch, lib, dev, spec=None):
         from oracle import qmm4_oracle as O  # synthetic-input generator only
 
-        idx, rows, k, n, sigma = WORKLOADS[name]
+        idx, rows, k, n, sigma = spec if spec is not None else WORKLOADS[name]
         self.name, self.rows, self.k, self.n = name, rows, k, n
         x, w, s, b = O.make_inputs(max(rows), k, n, sigma=sigma, seed=idx)
         wbytes = n * k // 2 + 4 * n * (k // 64)
@@ -230,6 +241,55 @@ def measure_layer_tail(torch, dev, rows_list=(4, 64), n_layers: int = 2, samples
     return out
 
 
+def measure_mid(torch, lib, dev, samples: int) -> dict:
+    """Per-call medians (HIP events per launch, rotating weight copies) of the up and down
+    projections at 65 to 2048 rows, with HBM and bf16-MFMA fractions of peak."""
+    out = {}
+    for name, spec in MID.items():
+        wl = Workload(name, torch, lib, dev, spec=spec)
+        for _ in range(2):
+            wl.step()
+        torch.cuda.synchronize()
+        for m in wl.rows:
+            ts = time_launches(torch, wl, m, samples)
+            med = statistics.median(ts)
+            byt, fl = bytes_per_call(m, wl.k, wl.n), 2 * m * wl.n * wl.k
+            hf, mf = byt / med / 1e9 / HBM_PEAK_GBS, fl / med / 1e12 / MFMA_BF16_PEAK_TFLOPS
+            out[f"{name} M={m}"] = {"shape": f"{m}x{wl.k}->{wl.n}", "us": round(med * 1e6, 2),
+                                    "hbm_frac": round(hf, 4), "mfma_frac": round(mf, 4),
+                                    "max_frac": round(max(hf, mf), 4), "samples": len(ts)}
+            log(f"[bench]   {name} M={m}: {med * 1e6:8.2f} us  HBM {hf:.1%}  MFMA {mf:.1%}")
+        del wl
+        torch.cuda.empty_cache()
+    return out
+
+
+def profile_figures() -> dict:
+    """The committed rocprofv3 figures for the headline kernel: its average duration in the kernel
+    trace of the default bench run, and its HBM bytes per launch from the counter passes (null
+    when the summary is absent or names another kernel)."""
+    out = {"trace_mean_us": None, "traffic": None, "traffic_kernel": None}
+    tpath = os.path.join(ROOT, "profiles", TRACE_PROFILE)
+    if os.path.exists(tpath):
+        with open(tpath) as f:
+            for ln in f:
+                if ln.startswith(f"head_kernel_mean_us {HEAD_KERNEL}:"):
+                    out["trace_mean_us"] = float(ln.rsplit(":", 1)[1])
+    cpath = os.path.join(ROOT, "profiles", TRAFFIC_PROFILE)
+    if os.path.exists(cpath):
+        kernel, traffic = None, None
+        with open(cpath) as f:
+            for ln in f:
+                if ln.startswith("Kernel:"):
+                    kernel = ln.split(":", 1)[1].strip()
+                if ln.startswith("hbm_bytes_per_launch:"):
+                    traffic = int(float(ln.split(":", 1)[1]))
+        out["traffic_kernel"] = kernel
+        if kernel is not None and HEAD_KERNEL in kernel:
+            out["traffic"] = traffic
+    return out
+
+
 def time_launches(torch, wl: Workload, m: int, samples: int) -> list[float]:
     """Per-launch kernel time (s) from HIP event pairs on the launch stream."""
     evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(samples)]
@@ -323,6 +383,7 @@ def main() -> int:
     ap.add_argument("--only", default="c0,c1,c2,c3,c4", help="workloads to measure (c1 is the headline)")
     ap.add_argument("--samples", type=int, default=30, help="single-launch samples per workload")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-mid", action="store_true", help="skip the mid-size M rows")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", default=None, metavar="WORKLOAD",
                     help="launch-only mode for rocprofv3: run WORKLOAD's steps --steps times, then a plain "
@@ -379,6 +440,10 @@ def main() -> int:
             torch.cuda.empty_cache()
 
     wl, res = head
+    mid = {}
+    if not args.no_mid:
+        log("[bench] mid-size M: up and down projections at 65 to 2048 rows")
+        mid = measure_mid(torch, lib, dev, args.samples)
     log("[bench] fused ops either side of the projection")
     fused = measure_fused(torch, lib, dev, wl)
     log("[bench] verify-forward layer tails (MLP half), eager and graph-captured")
@@ -411,15 +476,12 @@ def main() -> int:
         durs.append(a.elapsed_time(b) * 1e-3)
         byts.append(bytes_per_call(m, wl.k, wl.n))
     achieved = sum(byts) / sum(durs) / 1e9
-    traffic = None
     # HBM bytes per launch of the dominant kernel, from the committed rocprofv3 FETCH_SIZE and
-    # WRITE_SIZE passes (scaled by a copy of known size); null when that summary is absent.
-    tpath = os.path.join(ROOT, "profiles", "rowsplit_decode_gate_up_traffic.txt")
-    if os.path.exists(tpath):
-        with open(tpath) as f:
-            for ln in f:
-                if ln.startswith("hbm_bytes_per_launch:"):
-                    traffic = int(float(ln.split(":", 1)[1]))
+    # WRITE_SIZE passes (scaled by a copy of known size), and its trace duration.
+    prof = profile_figures()
+    mean_bytes = statistics.mean(byts)
+    trace_frac = (round(mean_bytes / (prof["trace_mean_us"] * 1e-6) / 1e9 / HBM_PEAK_GBS, 4)
+                  if prof["trace_mean_us"] else None)
 
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -430,12 +492,19 @@ def main() -> int:
                                "= the three calls", "M": [1, 2, 4], "K": 5120, "N": 34816, "group_size": 64,
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "qmm4::rowsplit_kernel<4, false> (rows <= 4, one workgroup per CU owning 136 weight "
-                               "rows)",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": prof["traffic"],
+                     "kernel": f"qmm4::{HEAD_KERNEL} (rows <= 4, one workgroup per CU owning 136 weight rows)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
-                     "bytes_per_launch": round(statistics.mean(byts))},
+                     "bytes_per_launch": round(mean_bytes),
+                     "trace_mean_us": prof["trace_mean_us"], "frac_trace": trace_frac,
+                     "event_overhead_us": (round(statistics.mean(durs) * 1e6 - prof["trace_mean_us"], 3)
+                                           if prof["trace_mean_us"] else None),
+                     "note": "achieved/frac: HIP events around each launch on the launch stream (they include "
+                             "the dispatch); trace_mean_us/frac_trace: the kernel's average duration in the "
+                             "committed rocprofv3 kernel trace of the default bench run; traffic: the committed "
+                             "FETCH_SIZE/WRITE_SIZE passes, null unless they name this kernel"},
         "workloads": out_workloads,
+        "mid_m": mid,
         "fused": fused,
     }
     if not args.no_cpu:

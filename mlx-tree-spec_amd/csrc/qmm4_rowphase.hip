@@ -52,6 +52,7 @@ struct RowPhaseParams {
   int BW;         // blocks per range
   int S;          // workgroups per range (K split)
   int NP;         // phases along K
+  int ranges;     // block ranges
 };
 
 template <int MB_, int V_, int BPW_, int W_>
@@ -98,8 +99,14 @@ void rowphase_kernel(RowPhaseParams P) {
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int n = lane & 15, g = lane >> 4;
-  const int p = blockIdx.x;
-  const int range = p / P.S, split = p - range * P.S;
+  // K split: workgroups that share a K slice of x sit on one XCD where the grid allows (workgroup
+  // b runs on XCD b % 8; the XCD-major order q = (b % 8) * (G / 8) + b / 8 walks splits
+  // outermost), so the slice is read from HBM into that XCD's L2 once instead of once per range.
+  const int G = gridDim.x;
+  const int q = (P.S > 1 && (G & 7) == 0) ? (int)((blockIdx.x & 7) * (G >> 3) + (blockIdx.x >> 3)) : (int)blockIdx.x;
+  const int split = P.S > 1 ? q / P.ranges : 0;
+  const int range = P.S > 1 ? q - split * P.ranges : q;
+  const int p = range * P.S + split;  // the partial tile's slot (range-major: the reduce kernel's order)
   const int b0 = range * P.BW;
   const int nbr = min(P.BW, P.NB - b0);  // blocks in this range
   const int pa = (int)((long long)split * P.NP / P.S);
@@ -556,7 +563,7 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
   RowPhaseParams P;
   P.x = x; P.s = s; P.b = b; P.w = w; P.y = y; P.part = part;
   P.M = M; P.N = N; P.K = K;
-  P.NB = N / 16; P.BW = plan.BW; P.S = plan.S; P.NP = plan.NP;
+  P.NB = N / 16; P.BW = plan.BW; P.S = plan.S; P.NP = plan.NP; P.ranges = plan.ranges;
   const void* f = rowphase_func(plan.variant);
   if (!f) return hipErrorInvalidValue;
   hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)plan.lds);
