@@ -365,6 +365,14 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
     return QMM4_OK;
   }
 
+  // 9 to 16 rows over a small problem (at most 32 weight rows per CU, K <= 6144): the row-split
+  // kernel's form with x straight into registers, every load in flight from the start.
+  if (rowsplit_xreg_plan((int)M, (int)N, (int)K, di->cus, &rplan)) {
+    e = launch_rowsplit(rplan, xb, w, sb, bb, yb, nullptr, nullptr, (int)M, (int)N, (int)K, stream);
+    if (e != hipSuccess) return hip_error(e, "row-split kernel launch");
+    return QMM4_OK;
+  }
+
   // A unit spans V super-steps; V must divide K / 128, and a unit's 2V scales (biases) of a row
   // are read with one 4V-byte load, so the scale and bias pointers must be 4V-byte aligned.
   int vmax = 4;

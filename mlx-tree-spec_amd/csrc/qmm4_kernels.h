@@ -80,6 +80,7 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
 struct RowSplitPlan {
   int MP;       // x rows per A fragment (4 or 8)
   bool small;   // every unit in flight from the start, all of x in LDS, sums in registers
+  bool xreg;    // 9-16 rows over a small problem: x loaded straight into registers per K chunk
   int V;        // super-steps (128 k) per unit
   bool fused;   // fused gate+up: y = silu(x w_gate^T) * (x w_up^T), w = [w_gate; w_up]
   int Nout;     // output columns (N, or N / 2 when fused)
@@ -96,6 +97,9 @@ struct RowSplitPlan {
 // Fills `plan` and returns true when the shape suits the row-split kernel on `cus` CUs. N is the
 // number of weight rows (for the fused gate+up, both halves).
 bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan);
+// 9 to 16 rows over at most 32 weight rows per CU and K of at most 6144: one wave per 512-k chunk
+// of both of its workgroup's blocks, x loaded straight into registers.
+bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan);
 // part / cnt: the workspace (plan.part_bytes, plan.ranges counters at zero) when plan.KS > 1.
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,

@@ -434,7 +434,173 @@ void rowsplit_kernel(RowSplitParams P) {
   if (tid == 0) __hip_atomic_store(&P.cnt[range], 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Up to 16 rows of x over a small problem, whole K per workgroup, x never staged: workgroup p owns
+// the R <= 32 rows [p R, p R + R) (RB <= 2 blocks of 16) and has one wave per K chunk of 512 k
+// (at most 12: K <= 6144, three waves per SIMD, 170 registers each). Wave w computes chunk w for
+// every block: it loads the chunk's A fragments of x (16 rows x 512 k,
+// lane (m, g) holds x[min(m, M - 1)] at the MFMA's k) straight into registers, the chunk's weights,
+// scales and biases of both blocks, and runs the chunk's MFMAs with each A fragment feeding both
+// blocks. Every load of the workgroup is issued at the start and nothing waits for a barrier
+// before the first MFMA; the chunk sums meet in LDS (one slot per chunk and block) and are added
+// in chunk order (deterministic). One memory round trip plus the L2 reads of x bound such a
+// launch (a verify tile of 16 x 5120 over 5120 columns: 160 KB of x per CU from L2, 57 KB of
+// weights from HBM).
+constexpr int kXrV = 4;        // super-steps per chunk (512 k)
+constexpr int kXrMaxRB = 2;    // blocks per workgroup
+constexpr int kXrMaxWaves = 12;
+template <int NCH>
+__global__ __launch_bounds__(64 * kXrMaxWaves) __attribute__((amdgpu_waves_per_eu(3)))
+void rowsplit_xreg_kernel(RowSplitParams P) {
+  constexpr int V = kXrV;
+  extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
+  f32x4* part = reinterpret_cast<f32x4*>(lds);  // [chunk][block][4 groups][16 lanes]
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int n = lane & 15, g = lane >> 4;
+  const int SU = P.SU;  // chunks along K
+  const int RB = P.RB;
+  const int r0 = blockIdx.x * P.R;
+  const int r1 = min(P.N, r0 + P.R);
+  const int KG = P.K >> 6;
+  constexpr uint32_t kOut = 0x40000000u;  // past the end of every buffer (each below 1 GiB)
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
+  const int wrec = rsrc_bytes((unsigned long long)P.N * (P.K >> 1));
+  const int srec = rsrc_bytes((unsigned long long)P.N * KG * 2);
+  const uint32_t xrow = (uint32_t)min(n, P.M - 1) * (uint32_t)P.K * 2u;
+
+  u32x4 xa[NCH][V][4];
+  u32x4 wv[NCH][kXrMaxRB][V];
+  Scales<V> sv[NCH][kXrMaxRB], bv[NCH][kXrMaxRB];
+  // Issue every load of this wave's chunks: weights first (from HBM), then x (from L2).
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int st = wave + c * kXrMaxWaves;
+    const bool live = st < SU;
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(P.w), 0,
+                                                                        live ? wrec : 0, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.s), 0,
+                                                                        live ? srec : 0, kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.b), 0,
+                                                                        live ? srec : 0, kBufferRsrcWord3);
+#pragma unroll
+    for (int b = 0; b < kXrMaxRB; ++b) {
+      const int row = r0 + b * 16 + n;
+      const bool ok = b < RB && row < r1;
+      const uint32_t wo = ok ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
+      const uint32_t so = ok ? (uint32_t)row * (uint32_t)KG * 2u : kOut;
+#pragma unroll
+      for (int v = 0; v < V; ++v)
+        wv[c][b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + v * 64, live ? st * V * 64 : 0, 0);
+      sv[c][b] = load_scales<V>(rs, so, live ? st * 4 * V : 0);
+      bv[c][b] = load_scales<V>(rb, so, live ? st * 4 * V : 0);
+    }
+  }
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int st = wave + c * kXrMaxWaves;
+    const bool live = st < SU;
+#pragma unroll
+    for (int v = 0; v < V; ++v)
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt) {
+        const uint32_t off = live ? xrow + (uint32_t)(st * V * 128 + v * 128 + g * 32 + tt * 8) * 2u : 0x80000000u;
+        xa[c][v][tt] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+      }
+  }
+
+#pragma unroll
+  for (int c = 0; c < NCH; ++c) {
+    const int st = wave + c * kXrMaxWaves;
+    if (st >= SU) break;
+    f32x4 acc[kXrMaxRB];
+#pragma unroll
+    for (int b = 0; b < kXrMaxRB; ++b) acc[b] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    bool bad = false;
+#pragma unroll
+    for (int b = 0; b < kXrMaxRB; ++b)
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int e2 = 2 * v + (g >> 1);
+        bad |= !fast_scale_ok((sv[c][b].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
+      }
+    const bool fast = __builtin_amdgcn_ballot_w64(bad) == 0;
+#pragma unroll
+    for (int v = 0; v < V; ++v) {
+      const int e2 = 2 * v + (g >> 1);
+      float c1[kXrMaxRB], c2[kXrMaxRB], bf[kXrMaxRB];
+#pragma unroll
+      for (int b = 0; b < kXrMaxRB; ++b) {
+        const float sf = bf16_to_f32((sv[c][b].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
+        bf[b] = bf16_to_f32((bv[c][b].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
+        c1[b] = fast ? sf * 16777216.0f : sf;
+        c2[b] = fast ? sf * 1048576.0f : sf * 0.0625f;
+      }
+#pragma unroll
+      for (int tt = 0; tt < 4; ++tt)
+#pragma unroll
+        for (int b = 0; b < kXrMaxRB; ++b) {
+          if (b < RB) {
+            const u32x4 B = fast ? dequant_word_fast(wv[c][b][v][tt], c1[b], c2[b], bf[b])
+                                 : dequant_word(wv[c][b][v][tt], c1[b], c2[b], bf[b]);
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(xa[c][v][tt]), as_bf16x8(B), acc[b], 0, 0, 0);
+          }
+        }
+    }
+#pragma unroll
+    for (int b = 0; b < kXrMaxRB; ++b)
+      if (b < RB) part[((st * kXrMaxRB + b) * 4 + g) * 16 + n] = acc[b];
+  }
+  __syncthreads();
+
+  // y[m, col]: the chunk sums of the column's block in chunk order; output row m = 4 g + r.
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+  for (int it = tid; it < P.R * 4; it += (int)blockDim.x) {
+    const int c = it >> 2, gg = it & 3;
+    const int col = r0 + c;
+    if (col >= r1 || 4 * gg >= P.M) continue;
+    const int b = c >> 4, nn = c & 15;
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int st = 0; st < SU; ++st) {
+      const f32x4 v = part[((st * kXrMaxRB + b) * 4 + gg) * 16 + nn];
+      sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = 4 * gg + r;
+      if (m < P.M)
+        __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_rne(sum[r]), ry, (uint32_t)(m * P.N + col) * 2u, 0, 0);
+    }
+  }
+}
+
 }  // namespace
+
+bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
+  if (M < 9 || M > 16 || cus < 1 || K % (128 * kXrV) != 0) return false;
+  if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 30)) return false;
+  const int R = ((N + cus - 1) / cus + 3) / 4 * 4;
+  const int RB = (R + 15) / 16;
+  const int SU = K / (128 * kXrV);
+  if (RB > kXrMaxRB || SU > kXrMaxWaves) return false;
+  plan->MP = 16;
+  plan->small = true;
+  plan->xreg = true;
+  plan->V = kXrV;
+  plan->fused = false;
+  plan->Nout = N;
+  plan->R = R;
+  plan->RB = RB;
+  plan->SU = SU;
+  plan->KS = 1;
+  plan->Kp = K;
+  plan->ranges = (N + R - 1) / R;
+  plan->blocks = plan->ranges;
+  plan->part_bytes = 0;
+  plan->smem = (size_t)SU * kXrMaxRB * 4 * 16 * 16;
+  return true;
+}
 
 int rowsplit_mp(int M) { return M <= 4 ? 4 : 8; }
 
@@ -462,6 +628,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
         (size_t)S * 16 * MP <= (size_t)kRsSmallXP * kRsThreads) {
       plan->MP = MP;
       plan->small = true;
+      plan->xreg = false;
       plan->V = 4;
       plan->fused = false;
       plan->Nout = nout;
@@ -496,6 +663,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
     const int ranges = (nout + R - 1) / R;
     plan->MP = MP;
     plan->small = false;
+    plan->xreg = false;
     plan->V = V;
     plan->fused = fused;
     plan->Nout = nout;
@@ -541,6 +709,11 @@ hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, 
   return plan.V == 5 ? launch_rowsplit_k<MP, 5, false>(plan, P, stream) : launch_rowsplit_k<MP, 4, false>(plan, P, stream);
 }
 
+hipError_t launch_rowsplit_xreg(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
+  hipLaunchKernelGGL((rowsplit_xreg_kernel<1>), dim3(plan.blocks), dim3(64 * plan.SU), plan.smem, stream, P);
+  return hipGetLastError();
+}
+
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
                            hipStream_t stream) {
@@ -550,6 +723,7 @@ hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const ui
   P.M = M; P.N = N; P.K = K;
   P.Nout = plan.Nout; P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
   P.KS = plan.KS; P.Kp = plan.Kp; P.part = part; P.cnt = cnt;
+  if (plan.xreg) return launch_rowsplit_xreg(plan, P, stream);
   switch (plan.MP) {
     case 4: return launch_rowsplit_m<4>(plan, P, stream);
     case 8: return launch_rowsplit_m<8>(plan, P, stream);

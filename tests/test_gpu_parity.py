@@ -415,6 +415,43 @@ def test_rowsplit_small_and_eight_row_one_hot_is_exact_dequant(kind, m, n):
         assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
 
 
+# 9 to 16 rows over at most 32 weight rows per CU with K <= 6144: the row-split form with x loaded
+# straight into registers, one wave per 512-k chunk. 16 x 5120 over 5120 columns (c0: 20 rows per
+# workgroup, a half-live second block), 12 rows over 2048 (8 rows per workgroup), N = 8208 (a partial
+# last range), 9 rows (fragment rows 9-15 repeat row 8).
+@pytest.mark.parametrize("m,k,n", [(16, 5120, 5120), (12, 4096, 2048), (16, 2048, 8208), (9, 5120, 1024)])
+def test_rowsplit_xreg_shapes(m, k, n):
+    note(f"row-split x-in-registers {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 23 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split xreg {m}x{k}x{n}", (x, w, s, b))
+    assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
+@pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
+def test_rowsplit_xreg_one_hot_is_exact_dequant(kind):
+    """One-hot rows of x through the x-in-registers form: single dequantized weights, bit for bit."""
+    m, k, n = 16, 5120, 5120
+    rng = np.random.default_rng({"fast": 41, "mixed": 42, "slow": 43}[kind])
+    s, b = scale_bias_pairs(kind, n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in (0, 2550, 5120 - m):
+        ks = k0 + np.arange(m)
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), ks] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.empty((m, n), dtype=np.uint16)
+        for i, kk in enumerate(ks):
+            g = kk // 64
+            ref[i] = O.dequantize(w[:, 8 * g:8 * g + 8], s[:, g:g + 1], b[:, g:g + 1])[:, kk - 64 * g]
+        keep = (ref & 0x7F80) != 0  # subnormal bf16 weights test the MFMA, not the dequant
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 # ----------------------------------------------------------------------------- row-phase path
 # More than 16 rows (or up to 16 when N gives every wave its own blocks) take the row-phase kernel
 # (K a multiple of 512). Wide shapes give each workgroup whole rows over all of K (N = 16 * 2049
@@ -581,9 +618,10 @@ def test_capture_needs_existing_workspace():
     """Under graph capture a call that would have to allocate its split-K workspace returns
     QMM4_ERR_CAPTURE; after one eager call on the stream the same call captures and replays."""
     from mlx_tree_spec_amd import _lib
-    x, w, s, b = O.make_inputs(16, 5120, 512, seed=41)
+    m, n, k = 32, 1024, 5120  # the row-phase kernel with K split 20 ways: partial tiles in the workspace
+    x, w, s, b = O.make_inputs(m, k, n, seed=41)
     xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
-    y = torch.empty((16, 512), dtype=torch.bfloat16, device=DEV)
+    y = torch.empty((m, n), dtype=torch.bfloat16, device=DEV)
     lib = _lib.load()
     st = torch.cuda.Stream()
     g = torch.cuda.CUDAGraph()
@@ -593,19 +631,19 @@ def test_capture_needs_existing_workspace():
             warnings.simplefilter("ignore")  # the refused call leaves the captured graph empty
             with torch.cuda.graph(g, stream=st):
                 rc = lib.qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(),
-                                          y.data_ptr(), 16, 512, 5120, 64, 4, 1, st.cuda_stream)
+                                          y.data_ptr(), m, n, k, 64, 4, 1, st.cuda_stream)
     except RuntimeError:
         pass  # an empty or invalidated capture may fail to instantiate
     assert rc == _lib.QMM4_ERR_CAPTURE, rc
     torch.cuda.synchronize()
     with torch.cuda.stream(st):
         assert lib.qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), y.data_ptr(),
-                                    16, 512, 5120, 64, 4, 1, st.cuda_stream) == 0
+                                    m, n, k, 64, 4, 1, st.cuda_stream) == 0
     st.synchronize()
     g = torch.cuda.CUDAGraph()
     with torch.cuda.graph(g, stream=st):
         assert lib.qmm4_affine_bf16(xd.data_ptr(), wd.data_ptr(), sd.data_ptr(), bd.data_ptr(), y.data_ptr(),
-                                    16, 512, 5120, 64, 4, 1, st.cuda_stream) == 0
+                                    m, n, k, 64, 4, 1, st.cuda_stream) == 0
     ref = O.quantized_matmul_exact(x, w, s, b)
     for rep in range(3):
         y.zero_()
