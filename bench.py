@@ -185,6 +185,35 @@ def measure_fused(torch, lib, dev, wl: Workload) -> dict:
         out[f"add_rms_norm rows={rows} D={d}"] = {"us": round(med * 1e6, 2), "gbs": round(byt / med / 1e9, 1),
                                                   "hbm_frac": round(byt / med / 1e9 / HBM_PEAK_GBS, 4), "bytes": byt}
         log(f"[bench]   add_rms_norm {rows}x{d}: {med * 1e6:8.2f} us  {byt / med / 1e9:7.1f} GB/s")
+    # The norm folded into the gate+up kernel (one launch) against the two calls it replaces
+    # (add_rms_norm, then gate_up_silu on its n); the same bits either way.
+    for m in wl.rows:
+        xs = [torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
+        rs = [torch.randn(m, d, generator=g).to(torch.bfloat16).to(dev) for _ in range(4)]
+        h, nn = torch.empty_like(xs[0]), torch.empty_like(xs[0])
+        y = torch.empty((m, n2), dtype=torch.int16, device=dev)
+
+        def pair(i, stream, m=m, xs=xs, rs=rs, h=h, nn=nn, y=y):
+            c, j = i % wl.copies, i % len(xs)
+            rc = lib.qmm4_add_rms_norm_bf16(xs[j].data_ptr(), rs[j].data_ptr(), w.data_ptr(), h.data_ptr(),
+                                            nn.data_ptr(), m, d, 1e-6, stream)
+            rc = rc or lib.qmm4_gate_up_silu_bf16(nn.data_ptr(), wl.w[c].data_ptr(), wl.s[c].data_ptr(),
+                                                  wl.b[c].data_ptr(), y.data_ptr(), m, wl.n, wl.k, 64, 4, 1, stream)
+            if rc != 0:
+                raise RuntimeError(f"add_rms_norm + gate_up_silu failed ({rc}): {lib.qmm4_last_error().decode()}")
+
+        def fold(i, stream, m=m, xs=xs, rs=rs, h=h, nn=nn, y=y):
+            c, j = i % wl.copies, i % len(xs)
+            rc = lib.qmm4_add_rms_norm_qmm_bf16(xs[j].data_ptr(), rs[j].data_ptr(), w.data_ptr(), 1e-6, h.data_ptr(),
+                                                nn.data_ptr(), wl.w[c].data_ptr(), wl.s[c].data_ptr(),
+                                                wl.b[c].data_ptr(), y.data_ptr(), m, wl.n, wl.k, 64, 4, 1, 1, stream)
+            if rc != 0:
+                raise RuntimeError(f"qmm4_add_rms_norm_qmm_bf16 failed ({rc}): {lib.qmm4_last_error().decode()}")
+
+        tp, tf = time_graph(torch, pair), time_graph(torch, fold)
+        out[f"add_rms_norm+gate_up_silu M={m}"] = {"two_calls_us": round(tp * 1e6, 2), "folded_us": round(tf * 1e6, 2),
+                                                   "saved_us": round((tp - tf) * 1e6, 2), "launches": "2 -> 1"}
+        log(f"[bench]   add_rms_norm + gate_up_silu M={m}: two calls {tp * 1e6:8.2f} us  folded {tf * 1e6:8.2f} us")
     return out
 
 

@@ -121,6 +121,32 @@ int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* bias
 int qmm4_add_rms_norm_bf16(const void* x, const void* r, const void* weight, void* h_out, void* n_out,
                            int64_t rows, int64_t D, float eps, void* hip_stream);
 
+/*
+ * (h, n, y) = (x + r, rmsnorm(x + r) * weight, projection of n) — the residual add + RMS norm and
+ * the quantized projection that consumes its output, as one call. Replaces the pair
+ * fused_ops.add_rms_norm (src/mlx_tree_spec/fused_ops.py:107-160) + the next layer's projection
+ * at tree_verify.py:444-446 (h, x = add_rms_norm(h, r, post_attention_layernorm); layer.mlp(x)).
+ *   epilogue QMM4_EPILOGUE_NONE:     y = n @ dequant(w)^T, bf16 [M, N]      (qmm4_affine_bf16)
+ *   epilogue QMM4_EPILOGUE_SILU_MUL: y = silu(n w_gate^T) * (n w_up^T), bf16 [M, N/2]
+ *                                                                          (qmm4_gate_up_silu_bf16)
+ *   x, r, h_out, n_out: bf16 [M, K]; weight: bf16 [K]; w, scales, biases as for qmm4_affine_bf16.
+ *   h_out, n_out and y hold exactly the bits of qmm4_add_rms_norm_bf16(x, r, weight, h_out, n_out,
+ *   M, K, eps) followed by qmm4_affine_bf16 / qmm4_gate_up_silu_bf16 on n_out. Up to 4 rows whose
+ *   projection runs as the row-split kernel (K <= 8192) take ONE launch: every workgroup forms h
+ *   and n for its own K slice in its x staging (the norm's launch and the n round trip through
+ *   memory disappear); other shapes run the two calls.
+ *   Requires the projection's conditions (and N % 32 == 0, y 16-byte aligned for SILU_MUL), the
+ *   norm's (K <= 16384, eps finite and >= 0, x, r, weight, h_out, n_out 16-byte aligned), and
+ *   h_out, n_out, y overlapping neither each other nor x, r, weight. M == 0 is a no-op; N == 0
+ *   runs the norm alone.
+ */
+#define QMM4_EPILOGUE_NONE 0
+#define QMM4_EPILOGUE_SILU_MUL 1
+int qmm4_add_rms_norm_qmm_bf16(const void* x, const void* r, const void* weight, float eps, void* h_out,
+                               void* n_out, const uint32_t* w, const void* scales, const void* biases, void* y,
+                               int64_t M, int64_t N, int64_t K, int group_size, int bits, int transpose,
+                               int epilogue, void* hip_stream);
+
 /* Message for the last non-zero return on this host thread ("" if none). */
 const char* qmm4_last_error(void);
 

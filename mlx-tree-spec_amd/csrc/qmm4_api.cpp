@@ -81,6 +81,12 @@ using qmm4::set_error;
 
 bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
 
+// Whether the byte ranges [a, a + an) and [b, b + bn) share a byte (empty ranges share none).
+bool overlaps(const void* a, size_t an, const void* b, size_t bn) {
+  const uintptr_t pa = reinterpret_cast<uintptr_t>(a), pb = reinterpret_cast<uintptr_t>(b);
+  return an > 0 && bn > 0 && pa < pb + bn && pb < pa + an;
+}
+
 // Whether work enqueued on `stream` now is being recorded into a graph (then nothing may be
 // allocated, freed or synchronized, and any buffer it uses must outlive the graph).
 int stream_capturing(hipStream_t stream, bool* capturing) {
@@ -450,9 +456,94 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
   return QMM4_OK;
 }
 
+int dispatch_norm_qmm(DeviceInfo* di, const void* x, const void* r, const void* weight, float eps, void* h_out,
+                      void* n_out, const uint32_t* w, const void* scales, const void* biases, void* y, int64_t M,
+                      int64_t N, int64_t K, bool silu_mul, hipStream_t stream, WorkspaceSource& ws) {
+  const uint16_t* xb = static_cast<const uint16_t*>(x);
+  uint16_t* nb = static_cast<uint16_t*>(n_out);
+  hipError_t e;
+  int rc;
+  // The plan dispatch_qmm / dispatch_gate_up_silu would take for n (the row-split kernel comes first
+  // in both for up to 8 rows), launched with the normalising x staging.
+  RowSplitPlan rplan;
+  if (N > 0 && M <= 4 && rowsplit_plan((int)M, (int)N, (int)K, di->cus, silu_mul, &rplan) &&
+      rowsplit_norm_ok(rplan, (int)M, (int)K)) {
+    uint32_t* cnt = nullptr;
+    float* part = nullptr;
+    if (rplan.KS > 1) {
+      rc = ws.get((size_t)rplan.ranges * sizeof(uint32_t), rplan.part_bytes, &cnt, &part);
+      if (rc) return rc;
+    }
+    const RowSplitNorm nm{static_cast<const uint16_t*>(r), static_cast<const uint16_t*>(weight),
+                          static_cast<uint16_t*>(h_out), nb, eps};
+    e = launch_rowsplit(rplan, xb, w, static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases),
+                        static_cast<uint16_t*>(y), part, cnt, (int)M, (int)N, (int)K, stream, &nm);
+    if (e != hipSuccess) return hip_error(e, "normalising row-split kernel launch");
+    return QMM4_OK;
+  }
+  e = launch_add_rms_norm(xb, static_cast<const uint16_t*>(r), static_cast<const uint16_t*>(weight),
+                          static_cast<uint16_t*>(h_out), nb, (int)M, (int)K, eps, stream);
+  if (e != hipSuccess) return hip_error(e, "add-rms-norm kernel launch");
+  if (N == 0) return QMM4_OK;
+  return silu_mul ? dispatch_gate_up_silu(di, n_out, w, scales, biases, y, M, N, K, stream, ws)
+                  : dispatch_qmm(di, n_out, w, scales, biases, y, M, N, K, stream, ws);
+}
+
 }  // namespace qmm4
 
 extern "C" {
+
+int qmm4_add_rms_norm_qmm_bf16(const void* x, const void* r, const void* weight, float eps, void* h_out,
+                               void* n_out, const uint32_t* w, const void* scales, const void* biases, void* y,
+                               int64_t M, int64_t N, int64_t K, int group_size, int bits, int transpose,
+                               int epilogue, void* hip_stream) {
+  qmm4::clear_error();
+  int rc = qmm4::check_qmm_args(x, w, scales, biases, y, M, N, K, group_size, bits, transpose);
+  if (rc) return rc;
+  if (epilogue != QMM4_EPILOGUE_NONE && epilogue != QMM4_EPILOGUE_SILU_MUL)
+    return set_error(QMM4_ERR_INVALID, "epilogue=%d: must be QMM4_EPILOGUE_NONE (0) or QMM4_EPILOGUE_SILU_MUL (1)",
+                     epilogue);
+  const bool silu_mul = epilogue == QMM4_EPILOGUE_SILU_MUL;
+  if (silu_mul && N % 32 != 0)
+    return set_error(QMM4_ERR_INVALID, "N=%lld must be a multiple of 32 (gate and up halves of whole 16-row blocks)",
+                     (long long)N);
+  if (K > qmm4::add_rms_norm_max_d())
+    return set_error(QMM4_ERR_INVALID, "K=%lld exceeds the norm's largest row of %d", (long long)K,
+                     qmm4::add_rms_norm_max_d());
+  if (!(eps >= 0.0f) || eps > 1e30f) return set_error(QMM4_ERR_INVALID, "eps must be finite and >= 0");
+  if (M == 0) return QMM4_OK;
+  if (!x || !r || !weight || !h_out || !n_out || (N > 0 && (!w || !scales || !biases || !y)))
+    return set_error(QMM4_ERR_INVALID, "null pointer argument");
+  if (!aligned(x, 16) || !aligned(r, 16) || !aligned(weight, 16) || !aligned(h_out, 16) || !aligned(n_out, 16))
+    return set_error(QMM4_ERR_INVALID, "x, r, weight, h_out and n_out must be 16-byte aligned");
+  if (silu_mul && N > 0 && !aligned(y, 16)) return set_error(QMM4_ERR_INVALID, "y must be 16-byte aligned");
+  // Every workgroup of the folded kernel reads all of x and r while the first writes h and n, and
+  // every workgroup writes y: the outputs may not overlap the inputs or each other.
+  const size_t rows_bytes = (size_t)M * (size_t)K * 2;
+  const size_t y_bytes = N > 0 ? (size_t)M * (size_t)(silu_mul ? N / 2 : N) * 2 : 0;
+  const struct {
+    const void* p;
+    size_t n;
+  } in[] = {{x, rows_bytes}, {r, rows_bytes}, {weight, (size_t)K * 2}}, out[] = {{h_out, rows_bytes},
+                                                                                   {n_out, rows_bytes},
+                                                                                   {y, y_bytes}};
+  for (const auto& o : out) {
+    for (const auto& i : in)
+      if (overlaps(o.p, o.n, i.p, i.n)) return set_error(QMM4_ERR_INVALID, "h_out, n_out and y may not overlap x, r or weight");
+    for (const auto& o2 : out)
+      if (&o2 != &o && overlaps(o.p, o.n, o2.p, o2.n))
+        return set_error(QMM4_ERR_INVALID, "h_out, n_out and y may not overlap each other");
+  }
+  hipStream_t stream = static_cast<hipStream_t>(hip_stream);
+  int dev = 0;
+  if ((rc = current_device(&dev))) return rc;
+  std::lock_guard<std::mutex> lock(qmm4::api_mutex());
+  qmm4::DeviceInfo* di = nullptr;
+  if ((rc = qmm4::device_info(dev, &di))) return rc;
+  StreamWorkspace ws(dev, stream);
+  return qmm4::dispatch_norm_qmm(di, x, r, weight, eps, h_out, n_out, w, scales, biases, y, M, N, K, silu_mul, stream,
+                                 ws);
+}
 
 int qmm4_add_rms_norm_bf16(const void* x, const void* r, const void* weight, void* h_out, void* n_out,
                            int64_t rows, int64_t D, float eps, void* hip_stream) {

@@ -53,6 +53,49 @@ __device__ __forceinline__ uint32_t silu_mul_bf16(uint32_t gbits, uint32_t ubits
   return bf16_rne(t * bf16_to_f32(ubits));
 }
 
+// The residual add + RMS norm of a row of D values (fused_ops.py:107-128), on 16-byte chunks of 8
+// values. The norm kernel and the row-split kernel's normalising x staging both use these, with the
+// same partition of a row over 256 threads, so they produce the same bits:
+//   norm_add_chunk    h = bf16(x + r) per value, and ss += h * h per value in order (fused
+//                     multiply-adds; a chunk of zeros leaves ss unchanged)
+//   norm_wave_sum     the 64 lanes' sums added by an xor butterfly (every lane gets the total)
+//   norm_inv          inv = 1 / sqrt(total / D + eps), correctly rounded division and square root
+//   norm_scale_chunk  n = bf16(w * bf16(h * inv)) per value
+__device__ __forceinline__ u32x4 norm_add_chunk(u32x4 a, u32x4 b, float& ss) {
+  u32x4 h;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t lo = bf16_rne(bf16_to_f32(a[e] & 0xFFFFu) + bf16_to_f32(b[e] & 0xFFFFu));
+    const uint32_t hi = bf16_rne(bf16_to_f32(a[e] >> 16) + bf16_to_f32(b[e] >> 16));
+    h[e] = lo | (hi << 16);
+    const float hl = bf16_to_f32(lo), hh = bf16_to_f32(hi);
+    ss = __builtin_fmaf(hl, hl, ss);
+    ss = __builtin_fmaf(hh, hh, ss);
+  }
+  return h;
+}
+
+__device__ __forceinline__ float norm_wave_sum(float ss) {
+#pragma unroll
+  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  return ss;
+}
+
+__device__ __forceinline__ float norm_inv(float total, int D, float eps) {
+  return __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(total, (float)D) + eps));
+}
+
+__device__ __forceinline__ u32x4 norm_scale_chunk(u32x4 h, u32x4 w, float inv) {
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float nl = bf16_to_f32(bf16_rne(bf16_to_f32(h[e] & 0xFFFFu) * inv));
+    const float nh = bf16_to_f32(bf16_rne(bf16_to_f32(h[e] >> 16) * inv));
+    o[e] = bf16_rne(bf16_to_f32(w[e] & 0xFFFFu) * nl) | (bf16_rne(bf16_to_f32(w[e] >> 16) * nh) << 16);
+  }
+  return o;
+}
+
 // Dequantize one packed word (codes for k = 8c .. 8c+7) with its group's scale and bias.
 // Result dword j holds bf16 for k = 8c+2j (low half) and 8c+2j+1 (high half).
 //

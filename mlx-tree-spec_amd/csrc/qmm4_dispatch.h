@@ -51,4 +51,12 @@ int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, cons
                           const void* biases, void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream,
                           WorkspaceSource& ws);
 
+// (h, n, y) = (x + r, rmsnorm(x + r) * weight, n @ dequant(w)^T), or the gate+up SiLU·mul of it
+// when `silu_mul`: the norm folded into the row-split kernel's x staging when its plan allows, else
+// the norm kernel followed by dispatch_qmm / dispatch_gate_up_silu on n (the same bits either way).
+// Arguments checked, M > 0, api_mutex held.
+int dispatch_norm_qmm(DeviceInfo* di, const void* x, const void* r, const void* weight, float eps, void* h_out,
+                      void* n_out, const uint32_t* w, const void* scales, const void* biases, void* y, int64_t M,
+                      int64_t N, int64_t K, bool silu_mul, hipStream_t stream, WorkspaceSource& ws);
+
 }  // namespace qmm4

@@ -63,39 +63,23 @@ __global__ __launch_bounds__(kNormThreads) void add_rms_norm_kernel(const uint16
     if (c < chunks) {
       const u32x4 a = *reinterpret_cast<const u32x4*>(x + base + c * 8);
       const u32x4 b = *reinterpret_cast<const u32x4*>(r + base + c * 8);
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t lo = bf16_rne(bf16_to_f32(a[e] & 0xFFFFu) + bf16_to_f32(b[e] & 0xFFFFu));
-        const uint32_t hi = bf16_rne(bf16_to_f32(a[e] >> 16) + bf16_to_f32(b[e] >> 16));
-        hv[i][e] = lo | (hi << 16);
-        const float hl = bf16_to_f32(lo), hh = bf16_to_f32(hi);
-        ss = __builtin_fmaf(hl, hl, ss);
-        ss = __builtin_fmaf(hh, hh, ss);
-      }
+      hv[i] = norm_add_chunk(a, b, ss);
       *reinterpret_cast<u32x4*>(h_out + base + c * 8) = hv[i];
     }
   }
-#pragma unroll
-  for (int off = 32; off > 0; off >>= 1) ss += __shfl_xor(ss, off);
+  ss = norm_wave_sum(ss);
   if ((tid & 63) == 0) red[tid >> 6] = ss;
   __syncthreads();
   float total = 0.0f;
 #pragma unroll
   for (int i = 0; i < kNormThreads / 64; ++i) total += red[i];
-  const float inv = __fdiv_rn(1.0f, __fsqrt_rn(__fdiv_rn(total, (float)D) + eps));
+  const float inv = norm_inv(total, D, eps);
 #pragma unroll
   for (int i = 0; i < CPT; ++i) {
     const int c = tid + i * kNormThreads;
     if (c < chunks) {
       const u32x4 wv = *reinterpret_cast<const u32x4*>(w + c * 8);
-      u32x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float nl = bf16_to_f32(bf16_rne(bf16_to_f32(hv[i][e] & 0xFFFFu) * inv));
-        const float nh = bf16_to_f32(bf16_rne(bf16_to_f32(hv[i][e] >> 16) * inv));
-        o[e] = bf16_rne(bf16_to_f32(wv[e] & 0xFFFFu) * nl) | (bf16_rne(bf16_to_f32(wv[e] >> 16) * nh) << 16);
-      }
-      *reinterpret_cast<u32x4*>(n_out + base + c * 8) = o;
+      *reinterpret_cast<u32x4*>(n_out + base + c * 8) = norm_scale_chunk(hv[i], wv, inv);
     }
   }
 }

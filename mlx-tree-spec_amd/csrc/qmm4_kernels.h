@@ -100,10 +100,23 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
 // 9 to 16 rows over at most 32 weight rows per CU and K of at most 6144: one wave per 512-k chunk
 // of both of its workgroup's blocks, x loaded straight into registers.
 bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan);
+// The residual add + RMS norm folded into the row-split kernel's x staging: the projection's
+// input is n = rmsnorm(x + r) * weight over rows of K, and h = x + r and n are also stored.
+struct RowSplitNorm {
+  const uint16_t* r;       // bf16 [M, K]
+  const uint16_t* weight;  // bf16 [K]
+  uint16_t* h;             // bf16 [M, K]
+  uint16_t* n;             // bf16 [M, K]
+  float eps;
+};
+// Whether a launch of `plan` can normalise its x while staging it (up to 4 rows, K <= 8192, not
+// the 9-16-row form).
+bool rowsplit_norm_ok(const RowSplitPlan& plan, int M, int K);
 // part / cnt: the workspace (plan.part_bytes, plan.ranges counters at zero) when plan.KS > 1.
+// `norm` (optional, rowsplit_norm_ok): x is normalised as it is staged.
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
-                           hipStream_t stream);
+                           hipStream_t stream, const RowSplitNorm* norm = nullptr);
 
 // y[m, j] = silu_mul_bf16(t[m, j], t[m, n + j]) for t bf16 [M, 2n] (the unfused gate+up epilogue).
 hipError_t launch_silu_mul(const uint16_t* t, uint16_t* y, int M, int n, hipStream_t stream);

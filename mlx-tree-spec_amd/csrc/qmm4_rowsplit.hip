@@ -60,6 +60,10 @@ constexpr int kRsXB = 4;  // x pieces per thread per staging batch
 // kRsSmallXP 16-byte pieces per thread: the whole LDS) is loaded global -> LDS directly.
 constexpr int kRsSmallXP = 10;
 constexpr size_t kRsLds = 160 * 1024;
+// NORM: each row of x is normalised by one group of 256 threads, 16-byte chunks t, t + 256, ... of
+// the row per thread, at most kRsNormChunks each (K <= 8192).
+constexpr int kRsNormThreads = 256;
+constexpr int kRsNormChunks = 4;
 
 struct RowSplitParams {
   const uint16_t* x;
@@ -76,6 +80,12 @@ struct RowSplitParams {
   int Kp;    // K per slice
   float* part;    // KS > 1: fp32 row sums [workgroup][row] (f32x4 over the rows of x)
   uint32_t* cnt;  // KS > 1: arrivals per column range (0 between launches)
+  // NORM: x is the residual stream's x, normalised while staged (see the kernel), with
+  const uint16_t* r;   // the residual rows, bf16 [M, K]
+  const uint16_t* nw;  // the norm weight, bf16 [K]
+  uint16_t* h_out;     // h = bf16(x + r), bf16 [M, K] (written by workgroup 0)
+  uint16_t* n_out;     // n = rmsnorm(h) * nw, bf16 [M, K] (written by workgroup 0)
+  float eps;
 };
 
 constexpr int kCoherent = 16;  // buffer access flag: bypass non-coherent caches (cross-CU partials)
@@ -105,17 +115,31 @@ __device__ __forceinline__ Scales<V> load_scales(__amdgpu_buffer_rsrc_t r, uint3
 __host__ __device__ inline size_t rowsplit_xs_bytes(int K, int MP) { return (size_t)(K >> 7) * 16 * MP * 16; }
 __host__ __device__ inline size_t rowsplit_part_bytes(int units, int MP) { return (size_t)units * (MP / 4) * 16 * 16; }
 
+// LDS offset of the NORM row sums (4 floats per row group): past x and, unless SMALL, past the
+// unit slots, the spare slot and the counter.
+__host__ __device__ inline size_t rowsplit_red_offset(int Kp, int MP, int units, bool small) {
+  return rowsplit_xs_bytes(Kp, MP) + (small ? 0 : rowsplit_part_bytes(units, MP) + 32);
+}
+
 // KSPLIT: K in P.KS slices (false: whole K, the slice arithmetic and the merge compiled out).
 // SMALL: a problem whose units all fit the waves' rings at once (U <= 32): wave w computes units
 // w and w + 16, both fetched at the start, then x goes straight into LDS; the sums stay in
 // registers until every wave is past its last x read and then take the unit slots over the x
 // area. Every load of such a launch is in flight from the start, which is what bounds small
 // problems (decode and small verify batches over a small N, e.g. 1-8 x 5120 x 5120).
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL>
+// NORM (up to 4 rows, K <= 8192): the residual add + RMS norm in front of the projection is folded
+// into the x staging, so that x = rmsnorm(x + r) * nw never leaves the CU. Thread group m (256
+// threads) of every workgroup forms row m of h = bf16(x + r) and its sum of squares over all of K
+// exactly as the norm kernel does (norm_add_chunk over the same chunks per thread, the butterfly,
+// then the 4 waves in order), so the staged rows are the bits that kernel would store for n, and y
+// is the bits of the unfused pair. Each workgroup reads all of x and r (from L2 after the first),
+// stages its K slice of n, and workgroup 0 writes h and n.
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   static_assert(MP == 4 || MP == 8, "x rows per fragment");
   static_assert(!SMALL || (!FUSED && !KSPLIT), "small plans are plain whole-K projections");
+  static_assert(!NORM || (MP == 4 && kRsThreads == MP * kRsNormThreads), "one thread group per normalised row");
   constexpr int G = MP / 4;  // lane groups holding output rows
   typedef f32x4 RowSums[G];  // the sums of one output column over x rows 4 g + r
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -188,12 +212,31 @@ void rowsplit_kernel(RowSplitParams P) {
       }
     }
   };
-  if constexpr (!SMALL) {
+  if constexpr (!SMALL && !NORM) {
     for (int bt = 0; bt + 1 < nxb; ++bt) {
       load_x(bt);
       store_x(bt);
     }
     load_x(nxb - 1);
+  }
+  // NORM: row grp of x and r, and the norm weight, for chunks c = tn + 256 i (rows >= M and chunks
+  // past the row read as zero).
+  const int grp = tid / kRsNormThreads, tn = tid - grp * kRsNormThreads;
+  u32x4 nx[kRsNormChunks], nr[kRsNormChunks], nwt[kRsNormChunks];
+  if constexpr (NORM) {
+    const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.r), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.nw), 0, rsrc_bytes((unsigned long long)P.K * 2), kBufferRsrcWord3);
+#pragma unroll
+    for (int i = 0; i < kRsNormChunks; ++i) {
+      const int c = tn + i * kRsNormThreads;
+      const bool live = grp < P.M && c < (P.K >> 3);
+      const uint32_t off = live ? ((uint32_t)grp * (uint32_t)P.K + (uint32_t)c * 8u) * 2u : 0x80000000u;
+      nx[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+      nr[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0);
+      nwt[i] = __builtin_amdgcn_raw_buffer_load_b128(rn, live ? (uint32_t)c * 16u : 0x80000000u, 0, 0);
+    }
   }
   // Every wave's x loads enter the CU's memory pipeline before any weight fetch: the pipeline
   // returns data in order, so an x load queued behind other waves' fetches would wait for them.
@@ -246,7 +289,40 @@ void rowsplit_kernel(RowSplitParams P) {
     __builtin_amdgcn_sched_barrier(0);
   }
 
-  if constexpr (SMALL) {
+  if constexpr (NORM) {
+    // h and the row's sum of squares, then the row sums of the group's 4 waves in wave order.
+    float* red = reinterpret_cast<float*>(lds + rowsplit_red_offset(P.Kp, MP, U, SMALL));
+    float ss = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRsNormChunks; ++i) nx[i] = norm_add_chunk(nx[i], nr[i], ss);
+    ss = norm_wave_sum(ss);
+    if (lane == 0) red[wave] = ss;
+    __syncthreads();
+    float total = 0.0f;
+#pragma unroll
+    for (int i = 0; i < kRsNormThreads / 64; ++i) total += red[grp * (kRsNormThreads / 64) + i];
+    const float inv = norm_inv(total, P.K, P.eps);
+    // n into the x stage (this workgroup's K slice: pieces kq / 8 .. kq / 8 + S * 16 - 1), and h, n
+    // to memory from workgroup 0.
+    const bool first = blockIdx.x == 0;
+#pragma unroll
+    for (int i = 0; i < kRsNormChunks; ++i) {
+      const int c = tn + i * kRsNormThreads;
+      if (grp < P.M && c < (P.K >> 3)) {
+        const u32x4 nv = norm_scale_chunk(nx[i], nwt[i], inv);
+        const int sq = c - (kq >> 3);
+        if (sq >= 0 && sq < S * 16) xs[sq * MP + grp] = nv;
+        if (first) {
+          const size_t o = (size_t)grp * P.K + (size_t)c * 8;
+          *reinterpret_cast<u32x4*>(P.h_out + o) = nx[i];
+          *reinterpret_cast<u32x4*>(P.n_out + o) = nv;
+        }
+      }
+    }
+    if constexpr (!SMALL) {
+      if (tid == 0) *next = kRsPF * kRsWaves;
+    }
+  } else if constexpr (SMALL) {
     // The weights (from HBM, the longest latency) went out first; x follows from L2. Every wave
     // waits for all of its loads, then the barrier publishes x.
     dma_x_all();
@@ -681,32 +757,42 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
   return false;
 }
 
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL = false>
+// Dynamic LDS of a launch: the plan's, plus the row sums of the normalising staging.
+size_t rowsplit_smem(const RowSplitPlan& plan, bool norm) {
+  if (!norm) return plan.smem;
+  return std::max(plan.smem, rowsplit_red_offset(plan.Kp, plan.MP, plan.RB * plan.SU, plan.small) +
+                                 sizeof(float) * (kRsThreads / 64));
+}
+
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM>
 hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRsLds);
+    hipError_t e = hipFuncSetAttribute(
+        reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM>),
+        hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRsLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL>), dim3(plan.blocks), dim3(kRsThreads), plan.smem,
-                     stream, P);
+  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM>), dim3(plan.blocks), dim3(kRsThreads),
+                     rowsplit_smem(plan, NORM), stream, P);
   return hipGetLastError();
 }
 
-template <int MP, int V, bool FUSED>
+template <int MP, int V, bool FUSED, bool NORM>
 hipError_t launch_rowsplit_k(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
-  return plan.KS > 1 ? launch_rowsplit_t<MP, V, FUSED, true>(plan, P, stream)
-                     : launch_rowsplit_t<MP, V, FUSED, false>(plan, P, stream);
+  return plan.KS > 1 ? launch_rowsplit_t<MP, V, FUSED, true, false, NORM>(plan, P, stream)
+                     : launch_rowsplit_t<MP, V, FUSED, false, false, NORM>(plan, P, stream);
 }
 
-template <int MP>
+template <int MP, bool NORM>
 hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
-  if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true>(plan, P, stream);
+  if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true, NORM>(plan, P, stream);
   if (plan.fused)
-    return plan.V == 5 ? launch_rowsplit_k<MP, 5, true>(plan, P, stream) : launch_rowsplit_k<MP, 4, true>(plan, P, stream);
-  return plan.V == 5 ? launch_rowsplit_k<MP, 5, false>(plan, P, stream) : launch_rowsplit_k<MP, 4, false>(plan, P, stream);
+    return plan.V == 5 ? launch_rowsplit_k<MP, 5, true, NORM>(plan, P, stream)
+                       : launch_rowsplit_k<MP, 4, true, NORM>(plan, P, stream);
+  return plan.V == 5 ? launch_rowsplit_k<MP, 5, false, NORM>(plan, P, stream)
+                     : launch_rowsplit_k<MP, 4, false, NORM>(plan, P, stream);
 }
 
 hipError_t launch_rowsplit_xreg(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
@@ -714,19 +800,31 @@ hipError_t launch_rowsplit_xreg(const RowSplitPlan& plan, const RowSplitParams& 
   return hipGetLastError();
 }
 
+bool rowsplit_norm_ok(const RowSplitPlan& plan, int M, int K) {
+  return !plan.xreg && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
+         K <= kRsNormThreads * kRsNormChunks * 8 && rowsplit_smem(plan, true) <= kRsLds;
+}
+
 hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, uint32_t* cnt, int M, int N, int K,
-                           hipStream_t stream) {
+                           hipStream_t stream, const RowSplitNorm* norm) {
   if (M > plan.MP) return hipErrorInvalidValue;
+  if (norm && !rowsplit_norm_ok(plan, M, K)) return hipErrorInvalidValue;
   RowSplitParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
   P.Nout = plan.Nout; P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
   P.KS = plan.KS; P.Kp = plan.Kp; P.part = part; P.cnt = cnt;
+  P.r = norm ? norm->r : nullptr;
+  P.nw = norm ? norm->weight : nullptr;
+  P.h_out = norm ? norm->h : nullptr;
+  P.n_out = norm ? norm->n : nullptr;
+  P.eps = norm ? norm->eps : 0.0f;
   if (plan.xreg) return launch_rowsplit_xreg(plan, P, stream);
+  if (norm) return launch_rowsplit_m<4, true>(plan, P, stream);
   switch (plan.MP) {
-    case 4: return launch_rowsplit_m<4>(plan, P, stream);
-    case 8: return launch_rowsplit_m<8>(plan, P, stream);
+    case 4: return launch_rowsplit_m<4, false>(plan, P, stream);
+    case 8: return launch_rowsplit_m<8, false>(plan, P, stream);
     default: return hipErrorInvalidValue;
   }
 }

@@ -18,6 +18,9 @@ QMM4_ERR_NOMEM = -12
 QMM4_ERR_HIP = -5
 QMM4_ERR_CAPTURE = -16
 
+QMM4_EPILOGUE_NONE = 0
+QMM4_EPILOGUE_SILU_MUL = 1
+
 # name -> (restype, argtypes); the symbols include/qmm4.h declares.
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64
@@ -28,6 +31,8 @@ SIGNATURES = {
     "qmm4_gate_up_silu_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, _i64, _int, _int, _int, _vp]),
     "dequant4_affine_bf16": (_int, [_vp, _vp, _vp, _vp, _i64, _i64, _int, _int, _vp]),
     "qmm4_add_rms_norm_bf16": (_int, [_vp, _vp, _vp, _vp, _vp, _i64, _i64, ctypes.c_float, _vp]),
+    "qmm4_add_rms_norm_qmm_bf16": (_int, [_vp, _vp, _vp, ctypes.c_float, _vp, _vp, _vp, _vp, _vp, _vp,
+                                          _i64, _i64, _i64, _int, _int, _int, _int, _vp]),
     "qmm4_last_error": (ctypes.c_char_p, []),
     "qmm4_abi_version": (_int, []),
 }

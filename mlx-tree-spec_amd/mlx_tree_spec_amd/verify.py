@@ -9,6 +9,8 @@ once over all rows, and each residual add is fused with the RMS norm that follow
     h, x = add_rms_norm(h, layer.mlp(x), nxt)                      # 446
 
 `r` is the attention (or GatedDeltaNet) output of the layer, which this package does not compute.
+When the MLP is a QuantizedMLP, the first norm is folded into its gate+up projection
+(add_rms_norm_gate_up: the same bits, one launch fewer for up to 4 rows).
 The row count M = the sum of the requests' tree nodes decides the kernel inside libqmm4 (row-split
 for M <= 4, verify kernels up to 64, the GEMM above), as packed_linear._call's routing does.
 
@@ -23,7 +25,8 @@ from __future__ import annotations
 
 import torch
 
-from .fused_ops import add_rms_norm
+from .fused_ops import add_rms_norm, add_rms_norm_gate_up
+from .packed_linear import STATS, QuantizedMLP
 
 
 class MLPLayer(torch.nn.Module):
@@ -37,8 +40,13 @@ class MLPLayer(torch.nn.Module):
 
 def layer_tail(h: torch.Tensor, r: torch.Tensor, layer: MLPLayer, next_norm: torch.nn.Module):
     """(h, x) after one layer's residual adds, norms and MLP (tree_verify.py:444-446)."""
+    mlp = layer.mlp
+    if isinstance(mlp, QuantizedMLP):
+        STATS["gate_up_silu"] += 1
+        h, _, t = add_rms_norm_gate_up(h, r, layer.post_attention_layernorm, mlp)
+        return add_rms_norm(h, mlp.down_proj(t), next_norm)
     h, x = add_rms_norm(h, r, layer.post_attention_layernorm)
-    return add_rms_norm(h, layer.mlp(x), next_norm)
+    return add_rms_norm(h, mlp(x), next_norm)
 
 
 def stack_tail(h: torch.Tensor, rs: list[torch.Tensor], layers: list[MLPLayer], final_norm: torch.nn.Module):

@@ -21,8 +21,8 @@ def declared_functions():
 
 def test_header_declares_expected_api():
     assert declared_functions() == sorted(["qmm4_affine_bf16", "qmm4_affine_bf16_noalloc", "qmm4_gate_up_silu_bf16",
-                                           "dequant4_affine_bf16", "qmm4_add_rms_norm_bf16", "qmm4_last_error",
-                                           "qmm4_abi_version"])
+                                           "dequant4_affine_bf16", "qmm4_add_rms_norm_bf16",
+                                           "qmm4_add_rms_norm_qmm_bf16", "qmm4_last_error", "qmm4_abi_version"])
 
 
 def test_library_exports_every_declared_symbol():
@@ -118,6 +118,43 @@ def test_add_rms_norm_rejects(rows, d, eps, ptr, msg):
 
 def test_add_rms_norm_empty_is_noop():
     assert _lib.load().qmm4_add_rms_norm_bf16(0, 0, 0, 0, 0, 0, 64, 1e-6, None) == _lib.QMM4_OK
+
+
+def call_norm_qmm(M=2, N=64, K=128, eps=1e-6, epilogue=0, gs=64, bits=4, x=0x100000, r=0x200000, nw=0x300000,
+                  h=0x400000, n=0x500000, w=0x600000, y=0x700000):
+    lib = _lib.load()
+    return lib.qmm4_add_rms_norm_qmm_bf16(x, r, nw, eps, h, n, w, w, w, y, M, N, K, gs, bits, 1, epilogue, None)
+
+
+@pytest.mark.parametrize("kw,code,msg", [
+    (dict(bits=8), _lib.QMM4_ERR_UNSUPPORTED, "bits=8"),
+    (dict(K=192), _lib.QMM4_ERR_INVALID, "K=192"),
+    (dict(N=24), _lib.QMM4_ERR_INVALID, "N=24"),
+    (dict(K=16512), _lib.QMM4_ERR_INVALID, "largest row"),
+    (dict(epilogue=2), _lib.QMM4_ERR_INVALID, "epilogue=2"),
+    (dict(epilogue=1, N=48), _lib.QMM4_ERR_INVALID, "multiple of 32"),
+    (dict(eps=-1.0), _lib.QMM4_ERR_INVALID, "eps"),
+    (dict(eps=float("inf")), _lib.QMM4_ERR_INVALID, "eps"),
+    (dict(r=0), _lib.QMM4_ERR_INVALID, "null pointer"),
+    (dict(h=0), _lib.QMM4_ERR_INVALID, "null pointer"),
+    (dict(n=0x500008), _lib.QMM4_ERR_INVALID, "16-byte aligned"),
+    (dict(nw=0x300004), _lib.QMM4_ERR_INVALID, "16-byte aligned"),
+    (dict(epilogue=1, y=0x700002), _lib.QMM4_ERR_INVALID, "y must be 16-byte aligned"),
+    (dict(h=0x100000), _lib.QMM4_ERR_INVALID, "overlap x, r or weight"),          # h on x
+    (dict(n=0x200000 + 256), _lib.QMM4_ERR_INVALID, "overlap x, r or weight"),    # n inside r
+    (dict(y=0x300000 + 64), _lib.QMM4_ERR_INVALID, "overlap x, r or weight"),     # y inside weight
+    (dict(n=0x400000 + 496), _lib.QMM4_ERR_INVALID, "overlap each other"),        # n's first row on h's last bytes
+    (dict(y=0x500000), _lib.QMM4_ERR_INVALID, "overlap each other"),
+])
+def test_norm_qmm_rejects(kw, code, msg):
+    """Every check of the folded norm + projection, before any device work (M=2, K=128: 512-byte rows)."""
+    assert call_norm_qmm(**kw) == code
+    assert msg in _lib.last_error()
+
+
+def test_norm_qmm_empty_is_noop():
+    assert call_norm_qmm(M=0, x=0, r=0, nw=0, h=0, n=0, w=0, y=0) == _lib.QMM4_OK
+    assert _lib.last_error() == ""
 
 
 def test_gate_up_empty_is_noop():

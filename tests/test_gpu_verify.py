@@ -32,7 +32,7 @@ def host_bits(t):
     return t.view(torch.int16).cpu().numpy().view(np.uint16)
 
 
-def make_stack(n_layers=2, seed=0):
+def make_stack(n_layers=2, seed=0, d=D, hdim=H):
     rng = np.random.default_rng(seed)
     layers, ref = [], []
 
@@ -41,18 +41,18 @@ def make_stack(n_layers=2, seed=0):
         return QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(sc), bf16_dev(b)), (w, sc, b)
 
     def norm():
-        wn = O.f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(D)).astype(np.float32))
-        m = torch.nn.RMSNorm(D, eps=EPS, device=DEV, dtype=torch.bfloat16)
+        wn = O.f32_to_bf16_bits((1 + 0.1 * rng.standard_normal(d)).astype(np.float32))
+        m = torch.nn.RMSNorm(d, eps=EPS, device=DEV, dtype=torch.bfloat16)
         with torch.no_grad():
             m.weight.copy_(bf16_dev(wn))
         return m, wn
 
     for i in range(n_layers):
         post, wpost = norm()
-        g, gw = lin(H, D, 100 * seed + 10 * i + 1)
-        u, uw = lin(H, D, 100 * seed + 10 * i + 2)
-        d, dw = lin(D, H, 100 * seed + 10 * i + 3)
-        layers.append(MLPLayer(post, QuantizedMLP(g, u, d)))
+        g, gw = lin(hdim, d, 100 * seed + 10 * i + 1)
+        u, uw = lin(hdim, d, 100 * seed + 10 * i + 2)
+        dn, dw = lin(d, hdim, 100 * seed + 10 * i + 3)
+        layers.append(MLPLayer(post, QuantizedMLP(g, u, dn)))
         gu = tuple(np.concatenate([a, c]) for a, c in zip(gw, uw))
         ref.append((wpost, gu, dw))
     final, wfinal = norm()
@@ -65,26 +65,28 @@ def oracle_stack(h, rs, ref, wfinal):
     for i, (wpost, gu, dw) in enumerate(ref):
         h, x = O.add_rms_norm(h, rs[i], wpost, EPS)
         t = O.f32_to_bf16_bits(cpu.qmm_f32(x, *gu))
-        a = O.silu_mul(t[:, :H], t[:, H:])
+        hh = t.shape[1] // 2
+        a = O.silu_mul(t[:, :hh], t[:, hh:])
         mo = O.f32_to_bf16_bits(cpu.qmm_f32(a, *dw))
         wn = ref[i + 1][0] if i + 1 < len(ref) else wfinal
         h, x = O.add_rms_norm(h, mo, wn, EPS)
     return h, x
 
 
-def inputs(rows, n_layers, seed):
+def inputs(rows, n_layers, seed, d=D):
     rng = np.random.default_rng(seed)
-    h = O.f32_to_bf16_bits(rng.standard_normal((rows, D)).astype(np.float32))
-    rs = [O.f32_to_bf16_bits((0.5 * rng.standard_normal((rows, D))).astype(np.float32)) for _ in range(n_layers)]
+    h = O.f32_to_bf16_bits(rng.standard_normal((rows, d)).astype(np.float32))
+    rs = [O.f32_to_bf16_bits((0.5 * rng.standard_normal((rows, d))).astype(np.float32)) for _ in range(n_layers)]
     return h, rs
 
 
 # M = the sum of the requests' tree nodes: one decode request of 3 nodes (row-split kernels), and
-# 4 requests x 16 nodes (verify kernels, two-pass gate+up).
-@pytest.mark.parametrize("rows", [3, 64])
-def test_stack_tail_matches_oracle_composition(rows):
-    layers, final, ref, wfinal = make_stack()
-    h, rs = inputs(rows, len(layers), rows)
+# 4 requests x 16 nodes (verify kernels, two-pass gate+up); at a width of 1024 and 8192 MLP
+# columns, 1 and 4 rows take the norm folded into the gate+up kernel.
+@pytest.mark.parametrize("rows,d,hdim", [(3, D, H), (64, D, H), (1, 1024, 8192), (4, 1024, 8192)])
+def test_stack_tail_matches_oracle_composition(rows, d, hdim):
+    layers, final, ref, wfinal = make_stack(d=d, hdim=hdim)
+    h, rs = inputs(rows, len(layers), rows, d)
     hg, xg = stack_tail(bf16_dev(h), [bf16_dev(r) for r in rs], layers, final)
     ho, xo = oracle_stack(h, rs, ref, wfinal)
     for got, want in ((hg, ho), (xg, xo)):
@@ -102,20 +104,20 @@ def check_tail(got, want, what):
         assert O.max_rel(g, w) <= O.MAX_REL_TOL and O.mean_rel(g, w) <= O.MEAN_REL_TOL
 
 
-@pytest.mark.parametrize("rows", [4, 64])
-def test_graphed_tail_replays_equal_eager(rows):
+@pytest.mark.parametrize("rows,d,hdim", [(4, D, H), (64, D, H), (4, 1024, 8192)])
+def test_graphed_tail_replays_equal_eager(rows, d, hdim):
     """Replays against the oracle's composition (not only against eager calls), with eager work of
     the same shape and of a larger shape on other streams between the replays."""
-    layers, final, ref, wfinal = make_stack(seed=1)
-    gt = GraphedTail(layers, final, rows, D, DEV)
+    layers, final, ref, wfinal = make_stack(seed=1, d=d, hdim=hdim)
+    gt = GraphedTail(layers, final, rows, d, DEV)
     side = torch.cuda.Stream()
     for rep in range(3):
-        h, rs = inputs(rows, len(layers), 1000 * rows + rep)
+        h, rs = inputs(rows, len(layers), 1000 * rows + rep, d)
         hd, rsd = bf16_dev(h), [bf16_dev(r) for r in rs]
         he, xe = stack_tail(hd, rsd, layers, final)  # eager work between the replays
         he, xe = host_bits(he), host_bits(xe)
         # A larger batch on another stream: its split-K workspace and scratch are that stream's.
-        hb, rsb = inputs(2 * rows + 7, len(layers), 7 + rep)
+        hb, rsb = inputs(2 * rows + 7, len(layers), 7 + rep, d)
         with torch.cuda.stream(side):
             stack_tail(bf16_dev(hb), [bf16_dev(r) for r in rsb], layers, final)
         side.synchronize()
