@@ -5,22 +5,32 @@
 // BN x BK block is dequantized once to bf16 (qmm_packed.py:629-637) into LDS and multiplied with
 // the BM x BK activation block; accumulation in fp32; bf16 out.
 //
-// Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 4 waves in a 2 x 2
-// arrangement (one per SIMD), each wave a 128 x 128 block of 4 x 4 MFMA 32x32x16 tiles (256 fp32
-// accumulators per lane). The larger wave tile reads each activation and weight fragment from LDS
-// for four MFMAs, so a K step moves 128 KB out of LDS instead of the 192 KB of 128 x 64 wave
-// tiles: LDS bandwidth, not the matrix cores, bounded the smaller tiles. LDS holds two stages of
-// [256][64 + 8] bf16 for the activations and for the dequantized weights (147 KB).
+// Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 8 waves in a 2 x 4
+// arrangement (two per SIMD, so one wave's loads, dequantization and LDS stores overlap the
+// other's MFMAs), each wave a 128 x 64 block of 4 x 2 MFMA 32x32x16 tiles (64 x 32 in the 128 x 128
+// tiles of stream-K and tail launches). LDS holds two stages of [BM][64 + 8] bf16 for the
+// activations and [BN][64 + 8] for the dequantized weights (147 KB at 256 x 256); the 144-byte
+// row pitch keeps the 16-byte fragment reads free of bank conflicts.
 //
-// Pipeline: the raw inputs of a K step (activation chunks, packed codes, scale and bias) are loaded
-// into registers two steps ahead of their use, through buffer resources (rows past M and columns
-// past N read as zero). While the MFMAs of step kt run from LDS stage kt % 2, the wave writes step
-// kt + 1 into the other stage: activations as loaded, weights dequantized exactly in registers
-// (dequant_word_fast; a thread whose group has a scale outside its range rewrites its words with
-// dequant_word after the MFMAs). One barrier per step. Workgroup ids are remapped so that
-// consecutive tiles land on one XCD and tiles are walked in groups of 4 row tiles, so a group
-// shares weight and activation blocks in L2. The output tile is staged through LDS and stored as
-// 16-byte row chunks.
+// Pipeline: the raw inputs of a K step (activation chunks, packed codes) are loaded into registers
+// two steps ahead of their use, through buffer resources (rows past M and columns past N read as
+// zero); scales and biases come 8 groups per 16-byte load when K % 512 == 0. While the MFMAs of
+// step kt run from LDS stage kt % 2, the waves write step kt + 1 into the other stage: activations
+// as loaded, weights dequantized exactly in registers (dequant_word_fast; a thread whose group has
+// a scale outside its range rewrites its words with dequant_word). One barrier per step.
+//
+// Work decomposition, chosen by gemm_plan:
+//  * More 128 x 128 tiles than CUs: whole 256 x 256 tiles, one per workgroup, in rounds of one per
+//    CU; when the last round would leave most CUs idle, its tiles are cut into 128 x 128 quarters in
+//    a second launch. Workgroup ids are remapped so that consecutive tiles land on one XCD, and
+//    tiles are walked in groups of 4 row tiles, so a group shares weight and activation blocks in
+//    L2.
+//  * At most one 128 x 128 tile per CU (65-256 rows of the model's projections): stream-K over
+//    128 x 128 tiles. The tiles x K units are split evenly over every resident workgroup (two per
+//    CU); a workgroup's first and last segments may cover part of a tile and leave fp32 partial
+//    tiles, which gemm_sk_reduce_kernel adds in K order (the same bits whichever workgroup ran a
+//    segment).
+// The output tile is staged through LDS and stored as 16-byte row chunks.
 #include <type_traits>
 
 #include "qmm4_common.h"
