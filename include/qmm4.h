@@ -51,11 +51,12 @@ extern "C" {
  *   (M + 256) * N * 2 bytes below 2^32), x and w 16-byte aligned, scales and biases
  *   4-byte aligned, y 2-byte aligned. M == 0 or N == 0 is a no-op. Rows M <= 64 run one of the
  *   HBM-bound verify/decode kernels (row-split for M <= 8 when its plan fits: whole K or a few K
- *   slices per workgroup, every unit in flight at once for small problems; row-phase for more
- *   than 16 rows, a large N, or fewer rows when its K split fills half the CUs; K-split verify or
- *   stream-K skinny otherwise), larger M the MFMA GEMM; the choice is a fixed function of the
- *   shape and the scale/bias alignment. Results are deterministic (bit-identical across calls and
- *   streams).
+ *   slices per workgroup, every unit in flight at once for small problems; its x-in-registers
+ *   form for 9-16 rows over small problems; row-phase for more than 16 rows, a large N, or fewer
+ *   rows when its K split fills half the CUs; K-split verify or stream-K skinny otherwise), larger
+ *   M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles when there are no
+ *   more tiles than CUs); the choice is a fixed function of the shape and the scale/bias
+ *   alignment. Results are deterministic (bit-identical across calls and streams).
  */
 int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
                      void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
@@ -137,8 +138,8 @@ int qmm4_add_rms_norm_bf16(const void* x, const void* r, const void* weight, voi
  *   memory disappear); other shapes run the two calls.
  *   Requires the projection's conditions (and N % 32 == 0, y 16-byte aligned for SILU_MUL), the
  *   norm's (K <= 16384, eps finite and >= 0, x, r, weight, h_out, n_out 16-byte aligned), and
- *   h_out, n_out, y overlapping neither each other nor x, r, weight. M == 0 is a no-op; N == 0
- *   runs the norm alone.
+ *   h_out, n_out, y overlapping neither each other nor x, r, weight, w, scales, biases. M == 0 is a
+ *   no-op; N == 0 runs the norm alone.
  */
 #define QMM4_EPILOGUE_NONE 0
 #define QMM4_EPILOGUE_SILU_MUL 1

@@ -521,15 +521,17 @@ int qmm4_add_rms_norm_qmm_bf16(const void* x, const void* r, const void* weight,
   // every workgroup writes y: the outputs may not overlap the inputs or each other.
   const size_t rows_bytes = (size_t)M * (size_t)K * 2;
   const size_t y_bytes = N > 0 ? (size_t)M * (size_t)(silu_mul ? N / 2 : N) * 2 : 0;
+  const size_t w_bytes = (size_t)N * (size_t)K / 2, sb_bytes = (size_t)N * (size_t)(K / 64) * 2;
   const struct {
     const void* p;
     size_t n;
-  } in[] = {{x, rows_bytes}, {r, rows_bytes}, {weight, (size_t)K * 2}}, out[] = {{h_out, rows_bytes},
-                                                                                   {n_out, rows_bytes},
-                                                                                   {y, y_bytes}};
+  } in[] = {{x, rows_bytes}, {r, rows_bytes}, {weight, (size_t)K * 2}, {w, w_bytes}, {scales, sb_bytes},
+            {biases, sb_bytes}},
+    out[] = {{h_out, rows_bytes}, {n_out, rows_bytes}, {y, y_bytes}};
   for (const auto& o : out) {
     for (const auto& i : in)
-      if (overlaps(o.p, o.n, i.p, i.n)) return set_error(QMM4_ERR_INVALID, "h_out, n_out and y may not overlap x, r or weight");
+      if (overlaps(o.p, o.n, i.p, i.n))
+        return set_error(QMM4_ERR_INVALID, "h_out, n_out and y may not overlap x, r, weight, w, scales or biases");
     for (const auto& o2 : out)
       if (&o2 != &o && overlaps(o.p, o.n, o2.p, o2.n))
         return set_error(QMM4_ERR_INVALID, "h_out, n_out and y may not overlap each other");

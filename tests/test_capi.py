@@ -140,9 +140,10 @@ def call_norm_qmm(M=2, N=64, K=128, eps=1e-6, epilogue=0, gs=64, bits=4, x=0x100
     (dict(n=0x500008), _lib.QMM4_ERR_INVALID, "16-byte aligned"),
     (dict(nw=0x300004), _lib.QMM4_ERR_INVALID, "16-byte aligned"),
     (dict(epilogue=1, y=0x700002), _lib.QMM4_ERR_INVALID, "y must be 16-byte aligned"),
-    (dict(h=0x100000), _lib.QMM4_ERR_INVALID, "overlap x, r or weight"),          # h on x
-    (dict(n=0x200000 + 256), _lib.QMM4_ERR_INVALID, "overlap x, r or weight"),    # n inside r
-    (dict(y=0x300000 + 64), _lib.QMM4_ERR_INVALID, "overlap x, r or weight"),     # y inside weight
+    (dict(h=0x100000), _lib.QMM4_ERR_INVALID, "overlap x, r, weight"),            # h on x
+    (dict(n=0x200000 + 256), _lib.QMM4_ERR_INVALID, "overlap x, r, weight"),      # n inside r
+    (dict(y=0x300000 + 64), _lib.QMM4_ERR_INVALID, "overlap x, r, weight"),       # y inside weight
+    (dict(h=0x600000 + 128), _lib.QMM4_ERR_INVALID, "overlap x, r, weight"),      # h inside w
     (dict(n=0x400000 + 496), _lib.QMM4_ERR_INVALID, "overlap each other"),        # n's first row on h's last bytes
     (dict(y=0x500000), _lib.QMM4_ERR_INVALID, "overlap each other"),
 ])
