@@ -53,6 +53,12 @@ MID = {
     "up": (6, (65, 128, 256, 512, 1024, 2048), 5120, 17408, 1.0),
     "down": (7, (65, 128, 256, 512, 1024, 2048), 17408, 5120, 0.5),
 }
+# One GPU's share of an 8-way split by output columns (the way the path would shard): the decode
+# gate+up and the vocab head at N / 8 columns. name: (seed, rows, K, N / 8, sigma)
+SHARD8 = {
+    "c1/8": (1, (1, 2, 4), 5120, 34816 // 8, 1.0),
+    "c3/8": (3, (32,), 5120, 151936 // 8, 1.0),
+}
 # The dominant kernel of the headline workload and the committed rocprofv3 summaries the roofline
 # record reads (the traffic figure is used only if its summary names this kernel).
 HEAD_KERNEL = "rowsplit_kernel<4, 4, false, false, false, false>"
@@ -296,6 +302,29 @@ def measure_mid(torch, lib, dev, samples: int) -> dict:
     return out
 
 
+def measure_shard8(torch, lib, dev, samples: int) -> dict:
+    """Per-call medians (HIP events per launch, rotating weight copies) of the decode gate+up and
+    vocab head at one GPU's share of an 8-way column split, with HBM fractions of peak."""
+    out = {}
+    for name, spec in SHARD8.items():
+        wl = Workload(name, torch, lib, dev, spec=spec)
+        for _ in range(2):
+            wl.step()
+        torch.cuda.synchronize()
+        for m in wl.rows:
+            ts = time_launches(torch, wl, m, samples)
+            med = statistics.median(ts)
+            byt = bytes_per_call(m, wl.k, wl.n)
+            hf = byt / med / 1e9 / HBM_PEAK_GBS
+            out[f"{name} M={m}"] = {"shape": f"{m}x{wl.k}->{wl.n}", "us": round(med * 1e6, 2),
+                                    "gbs": round(byt / med / 1e9, 1), "hbm_frac": round(hf, 4),
+                                    "samples": len(ts)}
+            log(f"[bench]   {name} M={m}: {med * 1e6:8.2f} us  HBM {hf:.1%}")
+        del wl
+        torch.cuda.empty_cache()
+    return out
+
+
 def profile_figures() -> dict:
     """The committed rocprofv3 figures for the headline kernel: its average duration in the kernel
     trace of the default bench run, and its HBM bytes per launch from the counter passes (null
@@ -476,6 +505,8 @@ def main() -> int:
     if not args.no_mid:
         log("[bench] mid-size M: up and down projections at 65 to 2048 rows")
         mid = measure_mid(torch, lib, dev, args.samples)
+    log("[bench] one GPU's share of an 8-way column split")
+    shard8 = measure_shard8(torch, lib, dev, args.samples)
     log("[bench] fused ops either side of the projection")
     fused = measure_fused(torch, lib, dev, wl)
     log("[bench] verify-forward layer tails (MLP half), eager and graph-captured")
@@ -537,6 +568,7 @@ def main() -> int:
                              "FETCH_SIZE/WRITE_SIZE passes, null unless they name this kernel"},
         "workloads": out_workloads,
         "mid_m": mid,
+        "shard8": shard8,
         "fused": fused,
     }
     if not args.no_cpu:

@@ -268,6 +268,19 @@ def test_workload_full(index, m):
     check_qmm(y, workload_ref(x, w, s, b), f"c{index} M={m}", (x, w, s, b))
 
 
+# One GPU's share of an 8-way column split (the path shards by output columns): the decode gate+up
+# at 34816 / 8 = 4352 columns and the vocab head at 151936 / 8 = 18992 columns, which is not a
+# multiple of 32 (a 16-column tail). The first and the last shard of the configs' own weights.
+@pytest.mark.parametrize("index,m,shard", [(1, 1, 0), (1, 4, 7), (3, 32, 0), (3, 32, 7)])
+def test_workload_one_gpu_share(index, m, shard):
+    note(f"workload {index} M={m} shard {shard} of 8")
+    x, w, s, b = O.config_inputs(index, m=m)
+    ns = w.shape[0] // 8
+    rows = slice(shard * ns, (shard + 1) * ns)
+    w, s, b = w[rows], s[rows], b[rows]
+    check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"c{index} M={m} shard {shard}", (x, w, s, b))
+
+
 def test_workload_prefill_sampled_rows():
     """The 4096 x 5120 -> 17408 prefill GEMM on the GPU; 256 sampled rows against the oracle."""
     x, w, s, b = O.config_inputs(4)
