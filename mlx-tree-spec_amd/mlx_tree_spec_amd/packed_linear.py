@@ -174,6 +174,14 @@ def _launcher(mod: QuantizedLinear):
 def _call(self: QuantizedLinear, x: torch.Tensor) -> torch.Tensor:
     sh = x.shape
     rows = math.prod(sh[:-1])
+    if "_fast" not in self.__dict__ and not eligible(self):
+        # packed_linear._call (84-86): a module the packed path does not take runs the general op
+        # (here quantized_matmul's dequantize + GEMM form for 4-bit shapes the kernels refuse; other
+        # formats raise NotImplementedError).
+        STATS["fallback"] += 1
+        y = quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
+                             group_size=self.group_size, bits=self.bits, mode=self.mode)
+        return y + self.bias if self.bias is not None else y
     STATS["skinny" if rows <= SKINNY_MAX_ROWS else "gemm"] += 1
     run = self.__dict__.get("_fast")
     y = run(x) if run is not None else None

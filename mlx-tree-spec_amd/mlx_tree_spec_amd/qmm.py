@@ -78,17 +78,28 @@ def aligned_contiguous(t: torch.Tensor, align: int = 16) -> torch.Tensor:
 def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor,
                      transpose: bool = True, group_size: int = 64, bits: int = 4,
                      mode: str = "affine") -> torch.Tensor:
-    """y = x @ dequant(w).T in bf16 with fp32 accumulation (HIP kernels; no fallback)."""
+    """y = x @ dequant(w).T in bf16 with fp32 accumulation (HIP kernels; no CPU path).
+
+    Shapes the packed kernels take (K % 128 == 0, N % 16 == 0) run them. Other shapes of the
+    format (K % 64 == 0, any N) are what the reference leaves to MLX's own op (packed_linear.py:
+    56-57, 84-86): the weights are dequantized exactly by the HIP kernel and multiplied by a bf16
+    GEMM with fp32 accumulation on the same stream.
+    """
     _check_format(group_size, bits, transpose, mode)
     if x.dtype != torch.bfloat16:
         raise ValueError(f"[quantized_matmul] x must be bfloat16, got {x.dtype}")
     if x.dim() < 1:
         raise ValueError("[quantized_matmul] x must have at least one dimension")
     k = x.shape[-1]
+    if k % group_size:
+        raise ValueError(f"[quantized_matmul] x.shape[-1]={k} must be a multiple of group_size={group_size}")
     n, _ = _check_weights(w, scales, biases, k, group_size, bits, "quantized_matmul")
     dev = _check_device("quantized_matmul", x, w, scales, biases)
     x2 = aligned_contiguous(x.reshape(-1, k))
     m = x2.shape[0]
+    if k % 128 or n % 16:
+        wd = dequantize(w, scales, biases, group_size, bits)
+        return torch.nn.functional.linear(x2, wd).reshape(*x.shape[:-1], n)
     w = aligned_contiguous(w)
     scales = aligned_contiguous(scales)
     biases = aligned_contiguous(biases)

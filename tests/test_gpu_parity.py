@@ -281,6 +281,36 @@ def test_workload_one_gpu_share(index, m, shard):
     check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"c{index} M={m} shard {shard}", (x, w, s, b))
 
 
+# Shapes of the format that the packed kernels do not take (K % 128 != 0, N % 16 != 0): the
+# reference leaves them to MLX's own op (packed_linear.py:84-86); here the HIP dequantization and a
+# bf16 GEMM with fp32 accumulation, held to the same tolerance against the oracle.
+@pytest.mark.parametrize("m,k,n", [(3, 192, 64), (70, 320, 48), (5, 128, 24), (1, 5120, 1000), (200, 64, 40)])
+def test_qmm_general_shapes(m, k, n):
+    note(f"general shape {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m + k + n)
+    check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"general {m}x{k}x{n}", (x, w, s, b))
+
+
+def test_quantized_linear_ineligible_module_falls_back():
+    """A module the packed path does not take (K % 128 != 0, or a linear bias) still computes
+    x @ dequant(w).T (+ bias), as the reference's _call does through MLX (packed_linear.py:84-86)."""
+    from mlx_tree_spec_amd import STATS, QuantizedLinear, eligible
+    x, w, s, b = O.make_inputs(6, 192, 96, seed=5)
+    mod = QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(s), bf16_dev(b))
+    assert not eligible(mod)
+    before = STATS["fallback"]
+    y = host_bits(mod(bf16_dev(x)))
+    assert STATS["fallback"] == before + 1
+    check_qmm(y, O.quantized_matmul_exact(x, w, s, b), "ineligible module", (x, w, s, b))
+    x2, w2, s2, b2 = O.make_inputs(4, 256, 64, seed=6)
+    bias = torch.linspace(-1, 1, 64, device=DEV).to(torch.bfloat16)
+    mb = QuantizedLinear.from_quantized(u32_dev(w2), bf16_dev(s2), bf16_dev(b2), bias=bias)
+    assert not eligible(mb)
+    got = O.bf16_bits_to_f32(host_bits(mb(bf16_dev(x2)))).astype(np.float64)
+    ref = O.bf16_bits_to_f32(O.quantized_matmul(x2, w2, s2, b2)).astype(np.float64) + bias.float().cpu().numpy()
+    assert O.max_rel(got, ref) <= O.MAX_REL_TOL
+
+
 def test_workload_prefill_sampled_rows():
     """The 4096 x 5120 -> 17408 prefill GEMM on the GPU; 256 sampled rows against the oracle."""
     x, w, s, b = O.config_inputs(4)

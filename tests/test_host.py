@@ -43,6 +43,10 @@ def test_shape_and_dtype_errors():
         quantized_matmul(x, w.float(), s, b)
     with pytest.raises(ValueError, match="both scales and biases"):
         quantized_matmul(x, w, s, None)
+    # K must be whole groups (x of 96 against weights of 96 codes per row: 12 words, one scale)
+    x96 = torch.zeros((2, 96), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="multiple of group_size"):
+        quantized_matmul(x96, torch.zeros((16, 12), dtype=torch.int32), s[:16, :1], b[:16, :1])
 
 
 def test_pack_nax_torch_matches_fixture_and_inverts():
