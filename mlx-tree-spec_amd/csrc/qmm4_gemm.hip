@@ -224,8 +224,16 @@ void gemm_kernel(GemmParams P) {
       const uint32_t w = d == 0 ? v.x : d == 1 ? v.y : d == 2 ? v.z : v.w;
       return (kt & 1) ? (w >> 16) : (w & 0xFFFFu);
     };
+    // Group G of a block held in registers, G known at compile time: a select on a run-time group
+    // would read both blocks' registers, one of them possibly still being loaded, and make the
+    // compiler wait for every load in flight at each step.
+    auto pick_c = [&](const u32x4& v, auto gc) __attribute__((always_inline)) {
+      constexpr int G = decltype(gc)::value;
+      const uint32_t w = G / 2 == 0 ? v.x : G / 2 == 1 ? v.y : G / 2 == 2 ? v.z : v.w;
+      return (G & 1) ? (w >> 16) : (w & 0xFFFFu);
+    };
     // Scale and bias bits of step kt for the weight stores.
-    auto sb_of = [&](const Raw<C>& R, int kt, uint32_t& sb, uint32_t& bb) __attribute__((always_inline)) {
+    auto sb_of =[&](const Raw<C>& R, int kt, uint32_t& sb, uint32_t& bb) __attribute__((always_inline)) {
       if constexpr (SB8) {
         sb = pick(scur, kt);
         bb = pick(bcur, kt);
@@ -264,18 +272,19 @@ void gemm_kernel(GemmParams P) {
 
     // Step kt: MFMAs from LDS stage kt % 2 while step kt + 1 (raw[(kt + 1) % 2]) is written into
     // the other stage; then step kt + 3 is loaded into the registers just written out.
-    auto step = [&](int kt, auto parity) {
+    auto step = [&](int kt, auto parity, auto ucst) {
       constexpr int ST = decltype(parity)::value;
+      constexpr int U = decltype(ucst)::value;  // SB8: kt % 8 (the loop is unrolled by 8)
       Raw<C>& R = raw[ST ^ 1];
-      if constexpr (SB8) {
-        // Step kt + 1 starts a block of 8 groups: move to it.
-        if (((kt + 1) & 7) == 0) {
-          scur = snext;
-          bcur = bnext;
-        }
-      }
       uint32_t sbits, bbits;
-      sb_of(R, kt + 1, sbits, bbits);
+      if constexpr (SB8) {
+        // Step kt + 1's group: of the current block, or the first of the next one (step 7).
+        constexpr int G1 = (U + 1) & 7;
+        sbits = pick_c(U < 7 ? scur : snext, std::integral_constant<int, G1>{});
+        bbits = pick_c(U < 7 ? bcur : bnext, std::integral_constant<int, G1>{});
+      } else {
+        sb_of(R, kt + 1, sbits, bbits);
+      }
       const uint16_t* as = As + ST * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
       const uint16_t* bs = Bs + ST * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
       // Fragments are double-buffered across the four 16-k sub-steps: sub-step ks + 1's reads are
@@ -306,7 +315,7 @@ void gemm_kernel(GemmParams P) {
       __syncthreads();
       load(kt + 3, R);
       if constexpr (SB8)
-        if (((kt + 3) & 7) == 0) load_sb8(kt + 3, snext, bnext);
+        if constexpr (U == 5) load_sb8(kt + 3, snext, bnext);  // the next block, first used at step 7
       // Keep these loads right behind the barrier (the scheduler would sink them toward their use
       // two steps later, into the middle of the next step's MFMAs).
       __builtin_amdgcn_sched_barrier(0);
@@ -326,9 +335,24 @@ void gemm_kernel(GemmParams P) {
     load(kb + 2, raw[0]);
     __syncthreads();
 
-    for (int kt = kb; kt < ke; kt += 2) {
-      step(kt, std::integral_constant<int, 0>{});
-      step(kt + 1, std::integral_constant<int, 1>{});
+    auto two = [&](int kt, auto u0) __attribute__((always_inline)) {
+      constexpr int U0 = decltype(u0)::value;
+      step(kt, std::integral_constant<int, 0>{}, std::integral_constant<int, U0>{});
+      step(kt + 1, std::integral_constant<int, 1>{}, std::integral_constant<int, U0 + 1>{});
+    };
+    if constexpr (SB8) {
+      // Unrolled by 8 (kb and ke are multiples of 8), so every step knows its group statically and
+      // the next block's registers become the current ones by a plain copy at the end.
+      for (int kt = kb; kt < ke; kt += 8) {
+        two(kt, std::integral_constant<int, 0>{});
+        two(kt + 2, std::integral_constant<int, 2>{});
+        two(kt + 4, std::integral_constant<int, 4>{});
+        two(kt + 6, std::integral_constant<int, 6>{});
+        scur = snext;
+        bcur = bnext;
+      }
+    } else {
+      for (int kt = kb; kt < ke; kt += 2) two(kt, std::integral_constant<int, 0>{});
     }
   };
 
