@@ -260,6 +260,31 @@ def test_gemm_stream_k_unaligned_scales():
     check_qmm(host_bits(y), O.quantized_matmul_exact(x, w, s, b), "stream-K unaligned scales", (x, w, s, b))
 
 
+# One-hot rows through each form of the GEMM with 8-group scale blocks (K % 512 == 0): stream-K with
+# tiles split between workgroups (128 rows), 128 x 128 quarter tiles (1024 rows), whole 256 x 256
+# tiles (2048 rows, where x is the identity). Each output is one dequantized weight, so every K
+# step's scale and bias group, in the fast and the general form, is checked bit for bit.
+@pytest.mark.parametrize("m,n", [(128, 4096), (1024, 8192), (2048, 8192)])
+@pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
+def test_gemm_one_hot_is_exact_dequant(kind, m, n):
+    note(f"GEMM one-hot {kind} {m}x2048x{n}")
+    k = 2048
+    rng = np.random.default_rng({"fast": 31, "mixed": 32, "slow": 33}[kind] + m)
+    s, b = scale_bias_pairs(kind, n * (k // 64), rng)
+    s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    deq = O.dequantize(w, s, b)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for k0 in range(0, k, m):
+        x = np.zeros((m, k), dtype=np.uint16)
+        x[np.arange(m), k0 + np.arange(m)] = 0x3F80  # 1.0
+        y = host_bits(quantized_matmul(bf16_dev(x), wd, sd, bd))
+        ref = np.ascontiguousarray(deq[:, k0:k0 + m].T)
+        keep = (ref & 0x7F80) != 0  # subnormal bf16 weights test the MFMA, not the dequant
+        bad = keep & (O.bf16_bits_to_f32(y) != O.bf16_bits_to_f32(ref))
+        assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
+
+
 @pytest.mark.parametrize("index,m", [(0, 16), (1, 1), (1, 2), (1, 4), (2, 64), (3, 32)])
 def test_workload_full(index, m):
     note(f"workload {index} M={m}")
