@@ -53,6 +53,12 @@ MID = {
     "up": (6, (65, 128, 256, 512, 1024, 2048), 5120, 17408, 1.0),
     "down": (7, (65, 128, 256, 512, 1024, 2048), 17408, 5120, 0.5),
 }
+# Every eligible linear of the target model (its seven (K, N) shapes) and its two vocabulary heads
+# (lm_head 5120 -> 248320, the drafter's 5120 -> 65984) at the decode (1, 4) and tree-verify
+# (16, 64) row counts. name: (seed, rows, K, N, sigma)
+MODEL = {f"{k}->{n}": (10 + i, (1, 4, 16, 64), k, n, 0.5 if k > 6144 else 1.0)
+         for i, (k, n) in enumerate([(5120, 17408), (17408, 5120), (5120, 10240), (5120, 6144), (6144, 5120),
+                                     (5120, 12288), (5120, 1024), (5120, 248320), (5120, 65984)])}
 # One GPU's share of an 8-way split by output columns (the way the path would shard): the decode
 # gate+up and the vocab head at N / 8 columns. name: (seed, rows, K, N / 8, sigma)
 SHARD8 = {
@@ -81,15 +87,33 @@ def bytes_per_call(m: int, k: int, n: int) -> int:
     return n * k // 2 + 2 * 2 * n * (k // 64) + 2 * m * k + 2 * m * n
 
 
+def _bf16_rne(a: np.ndarray) -> np.ndarray:
+    """fp32 -> bf16 bits, round to nearest even (the inputs drawn here are finite)."""
+    u = np.ascontiguousarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
+    return ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
+
+
+def synthetic_inputs(m: int, k: int, n: int, sigma: float = 1.0, seed: int = 0):
+    """The workloads' seeded synthetic inputs (numpy PCG64(seed), drawn in this order): x =
+    bf16(N(0, 1) * sigma) [m, k]; packed words uniform over uint32 [n, k / 8] (every 4-bit code iid
+    uniform 0..15); scales = bf16(|N(0, 1)| * 0.004 + 1e-4) and biases = bf16(-8 * scale +
+    N(0, 1) * 1e-3), [n, k / 64] each. Returns bf16 bit arrays (uint16) and the words (uint32)."""
+    rng = np.random.Generator(np.random.PCG64(seed))
+    x = _bf16_rne(rng.standard_normal((m, k), dtype=np.float32) * np.float32(sigma))
+    w = rng.integers(0, 2**32, size=(n, k // 8), dtype=np.uint32)
+    s = _bf16_rne(np.abs(rng.standard_normal((n, k // 64), dtype=np.float32)) * np.float32(0.004) + np.float32(1e-4))
+    sf = (s.astype(np.uint32) << 16).view(np.float32)
+    b = _bf16_rne(np.float32(-8.0) * sf + rng.standard_normal((n, k // 64), dtype=np.float32) * np.float32(1e-3))
+    return x, w, s, b
+
+
 class Workload:
     """Device-resident inputs of one benchmark workload with rotating weight copies."""
 
     def __init__(self, name: str, torch, lib, dev, spec=None):
-        from oracle import qmm4_oracle as O  # synthetic-input generator only
-
         idx, rows, k, n, sigma = spec if spec is not None else WORKLOADS[name]
         self.name, self.rows, self.k, self.n = name, rows, k, n
-        x, w, s, b = O.make_inputs(max(rows), k, n, sigma=sigma, seed=idx)
+        x, w, s, b = synthetic_inputs(max(rows), k, n, sigma=sigma, seed=idx)
         wbytes = n * k // 2 + 4 * n * (k // 64)
         self.copies = max(2, int(np.ceil(ROTATE_BYTES / wbytes)))
         t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(dev)
@@ -279,11 +303,12 @@ def measure_layer_tail(torch, dev, rows_list=(4, 64), n_layers: int = 2, samples
     return out
 
 
-def measure_mid(torch, lib, dev, samples: int) -> dict:
-    """Per-call medians (HIP events per launch, rotating weight copies) of the up and down
-    projections at 65 to 2048 rows, with HBM and bf16-MFMA fractions of peak."""
+def measure_rows(torch, lib, dev, samples: int, table: dict) -> dict:
+    """Per-call medians (HIP events per launch, rotating weight copies) of each shape of `table` at
+    its row counts, with HBM and bf16-MFMA fractions of peak: the up and down projections at 65 to
+    2048 rows (MID), every linear and head of the model at decode and verify rows (MODEL)."""
     out = {}
-    for name, spec in MID.items():
+    for name, spec in table.items():
         wl = Workload(name, torch, lib, dev, spec=spec)
         for _ in range(2):
             wl.step()
@@ -445,6 +470,7 @@ def main() -> int:
     ap.add_argument("--samples", type=int, default=30, help="single-launch samples per workload")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--no-mid", action="store_true", help="skip the mid-size M rows")
+    ap.add_argument("--no-model", action="store_true", help="skip the model's linears and heads")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--profile", default=None, metavar="WORKLOAD",
                     help="launch-only mode for rocprofv3: run WORKLOAD's steps --steps times, then a plain "
@@ -504,7 +530,11 @@ def main() -> int:
     mid = {}
     if not args.no_mid:
         log("[bench] mid-size M: up and down projections at 65 to 2048 rows")
-        mid = measure_mid(torch, lib, dev, args.samples)
+        mid = measure_rows(torch, lib, dev, args.samples, MID)
+    model = {}
+    if not args.no_model:
+        log("[bench] the model's linears and heads at decode and verify rows")
+        model = measure_rows(torch, lib, dev, args.samples, MODEL)
     log("[bench] one GPU's share of an 8-way column split")
     shard8 = measure_shard8(torch, lib, dev, args.samples)
     log("[bench] fused ops either side of the projection")
@@ -568,6 +598,7 @@ def main() -> int:
                              "FETCH_SIZE/WRITE_SIZE passes, null unless they name this kernel"},
         "workloads": out_workloads,
         "mid_m": mid,
+        "model_linears": model,
         "shard8": shard8,
         "fused": fused,
     }

@@ -471,8 +471,12 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
   X(5, 4, 2, 2, 8)                \
   X(6, 1, 4, 1, 8)                \
   X(7, 2, 4, 1, 8)                \
-  X(8, 4, 2, 1, 8)
-constexpr int kRpVariants = 9;
+  X(8, 4, 2, 1, 8)                \
+  X(9, 1, 2, 3, 8)                \
+  X(10, 2, 2, 3, 8)               \
+  X(11, 1, 2, 4, 8)               \
+  X(12, 2, 2, 4, 8)
+constexpr int kRpVariants = 13;
 
 #define QMM4_RPCFG(id, mb, v, bpw, w) typedef RpCfg<mb, v, bpw, w> RpCfg##id;
 QMM4_ROWPHASE_VARIANTS(QMM4_RPCFG)

@@ -309,6 +309,28 @@ def test_workload_one_gpu_share(index, m, shard):
 # Shapes of the format that the packed kernels do not take (K % 128 != 0, N % 16 != 0): the
 # reference leaves them to MLX's own op (packed_linear.py:84-86); here the HIP dequantization and a
 # bf16 GEMM with fp32 accumulation, held to the same tolerance against the oracle.
+# Every eligible linear of the target model (experiments/qmm_prefill.py:24-26: MLP gate/up and
+# down, GDN in_proj_qkv / in_proj_z / out_proj, attention q / k,v / o), its lm_head
+# (5120 -> 248320, tree_spec.py:645-677) and the drafter's head (N = 65984), at the row counts
+# the forward passes use: decode (1-4), tree verify (16-64 nodes), prompt tails (128, 512).
+# Inputs are drawn once per shape and sliced.
+MODEL_LINEARS = [(5120, 17408), (17408, 5120), (5120, 10240), (5120, 6144), (6144, 5120), (5120, 12288),
+                 (5120, 1024)]
+
+
+@pytest.mark.parametrize("k,n,rows", [(k, n, (1, 4, 16, 48, 64, 128, 512)) for k, n in MODEL_LINEARS]
+                         + [(5120, 248320, (1, 4, 16, 32)), (5120, 65984, (1, 4, 16, 32, 64))],
+                         ids=lambda v: str(v) if not isinstance(v, tuple) else "rows")
+def test_model_linear_shapes(k, n, rows):
+    x, w, s, b = O.make_inputs(max(rows), k, n, seed=k + n)
+    wd, sd, bd = u32_dev(w), bf16_dev(s), bf16_dev(b)
+    for m in rows:
+        note(f"model linear {m}x{k}x{n}")
+        xm = np.ascontiguousarray(x[:m])
+        y = host_bits(quantized_matmul(bf16_dev(xm), wd, sd, bd))
+        check_qmm(y, workload_ref(xm, w, s, b), f"model linear {m}x{k}x{n}", (xm, w, s, b))
+
+
 @pytest.mark.parametrize("m,k,n", [(3, 192, 64), (70, 320, 48), (5, 128, 24), (1, 5120, 1000), (200, 64, 40)])
 def test_qmm_general_shapes(m, k, n):
     note(f"general shape {m}x{k}x{n}")
@@ -524,16 +546,18 @@ def test_rowsplit_xreg_one_hot_is_exact_dequant(kind):
 # More than 16 rows (or up to 16 when N gives every wave its own blocks) take the row-phase kernel
 # (K a multiple of 512). Wide shapes give each workgroup whole rows over all of K (N = 16 * 2049
 # leaves the last range a partial one); narrow ones split K over the workgroups of a block range.
-# K = 3072 ends in a partial scale window.
+# K = 3072 ends in a partial scale window. 65984 columns (the drafter's head) give a workgroup 17
+# blocks (the 3-blocks-per-wave variants), 99984 and 131072 columns 25 and 32 blocks (4 per wave).
 @pytest.mark.parametrize("m,k,n", [(17, 5120, 4096), (33, 2048, 32784), (8, 5120, 34848), (48, 3072, 33024),
-                                   (64, 1024, 2064), (24, 17408, 1024)])
+                                   (64, 1024, 2064), (24, 17408, 1024), (16, 5120, 65984), (32, 2048, 65984),
+                                   (16, 5120, 99984), (32, 2048, 131072)])
 def test_rowphase_shapes(m, k, n):
     note(f"row-phase {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, seed=m * 11 + k + n)
     check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"row-phase {m}x{k}x{n}", (x, w, s, b))
 
 
-@pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48)])
+@pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48), (65984, 16), (131072, 32)])
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
     """One-hot rows of x on the row-phase path (wide and K-split): each output is one dequantized

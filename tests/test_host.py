@@ -85,3 +85,17 @@ def test_install_requires_device():
     model = torch.nn.Sequential(QuantizedLinear(256, 64), QuantizedLinear(128, 48))
     with pytest.raises(ValueError, match="HIP device"):
         install(model, verbose=False)
+
+
+@pytest.mark.parametrize("m,k,n,sigma,seed", [(4, 5120, 96, 1.0, 1), (64, 17408, 32, 0.5, 2), (3, 128, 16, 1.0, 0)])
+def test_bench_inputs_are_the_pinned_generator(m, k, n, sigma, seed):
+    """bench.py draws its workloads with its own generator (the oracle serves only its CPU baseline);
+    it must produce the same bits as the oracle's make_inputs, the generator the parity tests and
+    the committed fixtures use."""
+    import bench
+
+    got = bench.synthetic_inputs(m, k, n, sigma=sigma, seed=seed)
+    want = O.make_inputs(m, k, n, sigma=sigma, seed=seed)
+    for g, w in zip(got, want):
+        assert g.dtype == w.dtype and g.shape == w.shape
+        assert np.array_equal(g, w)
