@@ -518,21 +518,47 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   // kRpNarrowBpw blocks per wave, K split over the CUs.
   constexpr int kW = 8;  // waves per workgroup of every variant
   const bool wide = NB >= kW * cus;
-  const int want = wide ? ((NB + cus - 1) / cus + kW - 1) / kW : kRpNarrowBpw;
   // The variant for mb rows with the fewest blocks per wave that still holds `want` (or the most).
-  int id = -1, best_b = 0;
-  for (int c = 0; c < kRpVariants; ++c) {
-    int cm, cv, cb, items;
-    size_t l;
-    rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
-    if (cm != mb || ks % cv != 0) continue;
-    const bool fits = cb >= want;
-    const bool best_fits = best_b >= want;
-    if (id < 0 || (fits && (!best_fits || cb < best_b)) || (!fits && !best_fits && cb > best_b)) {
-      id = c;
-      best_b = cb;
+  auto pick = [&](int want) {
+    int id = -1, best_b = 0;
+    for (int c = 0; c < kRpVariants; ++c) {
+      int cm, cv, cb, items;
+      size_t l;
+      rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
+      if (cm != mb || ks % cv != 0) continue;
+      const bool fits = cb >= want;
+      const bool best_fits = best_b >= want;
+      if (id < 0 || (fits && (!best_fits || cb < best_b)) || (!fits && !best_fits && cb > best_b)) {
+        id = c;
+        best_b = cb;
+      }
     }
+    return id;
+  };
+  // Wide: a CU's share of the blocks in ranges of one size, as many per CU as the largest variant
+  // needs; the grid then holds about `passes` ranges per CU, which the hardware starts on each CU as
+  // the previous one ends. Ranges of the largest variant's size would leave a partial last round:
+  // lm_head 248320 x 5120 at 16 / 32 rows takes 388 ranges of 40 blocks in 226 / 250 us, 501 of 31
+  // in 206 / 229 us. Up to 32 rows only: every range reads all of x, and at 64 rows (655 KB of x
+  // per range at K = 5120) the extra ranges cost more than the balance gains (+4-7%).
+  int passes = 1, bw = (NB + cus - 1) / cus;
+  if (wide && mb <= 2) {
+    const int maxb = [&] {
+      int m = 0;
+      for (int c = 0; c < kRpVariants; ++c) {
+        int cm, cv, cb, items;
+        size_t l;
+        rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
+        if (cm == mb && ks % cv == 0 && cb > m) m = cb;
+      }
+      return m;
+    }();
+    if (maxb == 0) return false;
+    const int share = (NB + cus - 1) / cus;
+    passes = (share + kW * maxb - 1) / (kW * maxb);
+    bw = (NB + cus * passes - 1) / (cus * passes);
   }
+  const int id = pick(wide ? (bw + kW - 1) / kW : kRpNarrowBpw);
   if (id < 0) return false;
   int cm, v, bpw, items;
   size_t lds;
@@ -540,8 +566,7 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   const int NP = ks / v;
   int BW, S;
   if (wide) {
-    BW = (NB + cus - 1) / cus;
-    if (BW > kW * bpw) BW = kW * bpw;
+    BW = bw < kW * bpw ? bw : kW * bpw;
     S = 1;
   } else {
     BW = kW * bpw;
