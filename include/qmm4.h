@@ -50,13 +50,13 @@ extern "C" {
  *   w, x and y each below 4 GiB (with 256 rows of margin: (N + 256) * K / 2, (M + 256) * K * 2 and
  *   (M + 256) * N * 2 bytes below 2^32), x and w 16-byte aligned, scales and biases
  *   4-byte aligned, y 2-byte aligned. M == 0 or N == 0 is a no-op. Rows M <= 64 run one of the
- *   HBM-bound verify/decode kernels (row-split for M <= 8 when its plan fits: whole K or a few K
- *   slices per workgroup, every unit in flight at once for small problems; its x-in-registers
- *   form for 9-16 rows over small problems; row-phase for more than 16 rows, a large N, or fewer
- *   rows when its K split fills half the CUs; K-split verify or stream-K skinny otherwise), larger
- *   M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles when there are no
- *   more tiles than CUs); the choice is a fixed function of the shape and the scale/bias
- *   alignment. Results are deterministic (bit-identical across calls and streams).
+ *   HBM-bound verify/decode kernels (row-split's x-in-registers form for 9-16 rows over small
+ *   problems; row-split for M <= 16 when its plan fits: whole K or a few K slices per workgroup,
+ *   every unit in flight at once for small problems; row-phase for more than 16 rows, a large N,
+ *   or fewer rows when its K split fills half the CUs; K-split verify or stream-K skinny
+ *   otherwise), larger M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles
+ *   when there are no more tiles than CUs); the choice is a fixed function of the shape and the
+ *   scale/bias alignment. Results are deterministic (bit-identical across calls and streams).
  */
 int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
                      void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
@@ -91,7 +91,7 @@ int qmm4_affine_bf16_noalloc(const void* x, const uint32_t* w, const void* scale
  *   The gate and up sums are rounded to bf16 (the values the two projections would store), then
  *   out = bf16(bf16(g * bf16(sigmoid(g))) * u), one rounding per operation of the unfused
  *   composition. Same requirements as qmm4_affine_bf16, plus N % 32 == 0 and y 16-byte aligned.
- *   Up to 4 rows over a large N run as one kernel; otherwise the projection goes to a
+ *   Up to 16 rows whose row-split plan fits run as one kernel; otherwise the projection goes to a
  *   library-held [M, N] buffer (per device and stream, grown on demand) and the epilogue is a
  *   second pass. Deterministic.
  */

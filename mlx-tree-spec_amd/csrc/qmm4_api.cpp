@@ -356,9 +356,16 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
     return QMM4_OK;
   }
 
-  // Up to 4 rows and enough output columns to give every CU its own rows (whole K, or K in 2 or 4
-  // slices when N is small): the row-split kernel.
+  // 9 to 16 rows over a small problem (at most 32 weight rows per CU, K <= 6144): the row-split
+  // kernel's form with x straight into registers, every load in flight from the start.
   RowSplitPlan rplan;
+  if (M >= 9 && rowsplit_xreg_plan((int)M, (int)N, (int)K, di->cus, &rplan)) {
+    e = launch_rowsplit(rplan, xb, w, sb, bb, yb, nullptr, nullptr, (int)M, (int)N, (int)K, stream);
+    if (e != hipSuccess) return hip_error(e, "row-split kernel launch");
+    return QMM4_OK;
+  }
+  // Up to 16 rows and enough output columns to give every CU its own rows (whole K, or K in a few
+  // slices when N is small or x is large): the row-split kernel.
   if (rowsplit_plan((int)M, (int)N, (int)K, di->cus, false, &rplan)) {
     uint32_t* rcnt = nullptr;
     float* rpart = nullptr;
@@ -367,14 +374,6 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
       if (rc) return rc;
     }
     e = launch_rowsplit(rplan, xb, w, sb, bb, yb, rpart, rcnt, (int)M, (int)N, (int)K, stream);
-    if (e != hipSuccess) return hip_error(e, "row-split kernel launch");
-    return QMM4_OK;
-  }
-
-  // 9 to 16 rows over a small problem (at most 32 weight rows per CU, K <= 6144): the row-split
-  // kernel's form with x straight into registers, every load in flight from the start.
-  if (rowsplit_xreg_plan((int)M, (int)N, (int)K, di->cus, &rplan)) {
-    e = launch_rowsplit(rplan, xb, w, sb, bb, yb, nullptr, nullptr, (int)M, (int)N, (int)K, stream);
     if (e != hipSuccess) return hip_error(e, "row-split kernel launch");
     return QMM4_OK;
   }

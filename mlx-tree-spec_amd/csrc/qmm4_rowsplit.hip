@@ -20,7 +20,7 @@
 //    so each row is read as one contiguous run per unit. Rows past the workgroup's range read as
 //    zero (an offset outside the buffer resource), as do fetches past the last unit (a zero-length
 //    resource).
-//  * x (M <= MP rows, MP = 4 or 8, whole K or the workgroup's K slice) is staged once in LDS in
+//  * x (M <= MP rows, MP = 4, 8 or 16, whole K or the workgroup's K slice) is staged once in LDS in
 //    A-fragment order. Every wave issues its x loads before any wave issues a weight fetch (a bare
 //    barrier between the two), and the stores wait for the x loads alone (the vector memory
 //    counter is in order).
@@ -51,7 +51,7 @@ namespace {
 
 constexpr int kRsWaves = 16;
 constexpr int kRsThreads = 64 * kRsWaves;
-// MP: x rows held per A fragment (4 or 8; M <= MP). The MFMA's 16 rows are x rows
+// MP: x rows held per A fragment (4, 8 or 16; M <= MP). The MFMA's 16 rows are x rows
 // min(row, M - 1); output rows 4 g + r lie in lane group g, so a unit's sums live in the MP / 4
 // lane groups g < MP / 4.
 constexpr int kRsPF = 2;  // units in flight per wave
@@ -137,7 +137,7 @@ __host__ __device__ inline size_t rowsplit_red_offset(int Kp, int MP, int units,
 template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
-  static_assert(MP == 4 || MP == 8, "x rows per fragment");
+  static_assert(MP == 4 || MP == 8 || MP == 16, "x rows per fragment");
   static_assert(!SMALL || (!FUSED && !KSPLIT), "small plans are plain whole-K projections");
   static_assert(!NORM || (MP == 4 && kRsThreads == MP * kRsNormThreads), "one thread group per normalised row");
   constexpr int G = MP / 4;  // lane groups holding output rows
@@ -678,10 +678,10 @@ bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
   return true;
 }
 
-int rowsplit_mp(int M) { return M <= 4 ? 4 : 8; }
+int rowsplit_mp(int M) { return M <= 4 ? 4 : M <= 8 ? 8 : 16; }
 
 bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan) {
-  if (M < 1 || M > 8 || cus < 1) return false;
+  if (M < 1 || M > 16 || cus < 1) return false;
   if (fused && N % 32 != 0) return false;
   // Row offsets of this kernel stay below 1 GiB.
   if ((unsigned long long)(N + 256) * (unsigned long long)K / 2 >= (1ULL << 30)) return false;
@@ -689,8 +689,9 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
   const int nout = fused ? N / 2 : N;
   // Up to 4 rows: whole K per workgroup when the columns alone give every CU at least 4 row
   // blocks; otherwise K in 2 or 4 slices over as many workgroups per column range, when each
-  // workgroup still has at least 3 units per wave. 5 to 8 rows (a small verify batch): the fewest
-  // K slices whose x slice and unit slots fit in LDS.
+  // workgroup still has at least 3 units per wave. 5 to 16 rows (a verify batch of up to 16 tree
+  // nodes): the fewest K slices whose x slice and unit slots fit in LDS (up to 8 slices for 8
+  // rows, 4 for 16).
   // A problem whose units all fit the waves' rings at once, with all of x in LDS: the SMALL form
   // (every load in flight from the start, no K slices).
   if (!fused && K % 512 == 0) {
@@ -720,7 +721,9 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       return true;
     }
   }
-  const int max_ks = MP == 4 ? 4 : 8;
+  // 9 to 16 rows: at most 4 K slices (x slices of 16 rows are large; with 8 slices, e.g. the
+  // 65984-column head, the cross-workgroup merge of the slices costs more than it saves).
+  const int max_ks = MP == 8 ? 8 : 4;
   for (int ks = 1; ks <= max_ks; ks *= 2) {
     if (K % (128 * ks) != 0) continue;
     const int kp = K / ks;
@@ -825,6 +828,7 @@ hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const ui
   switch (plan.MP) {
     case 4: return launch_rowsplit_m<4, false>(plan, P, stream);
     case 8: return launch_rowsplit_m<8, false>(plan, P, stream);
+    case 16: return launch_rowsplit_m<16, false>(plan, P, stream);
     default: return hipErrorInvalidValue;
   }
 }

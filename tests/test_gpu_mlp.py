@@ -59,10 +59,12 @@ def check_gate_up(x, w, s, b):
     return y
 
 
-# Up to 4 rows over a large N: one row-split launch with the epilogue fused. N = 34848 leaves the
+# Up to 16 rows over a large N: one row-split launch with the epilogue fused. N = 34848 leaves the
 # last workgroup a partial range (17424 = 242 x 72); K = 4096 gives units of 4 super-steps, 5120 of 5.
+# 9 to 16 rows (a tree-verify batch) take 16-row fragments with K in slices.
 @pytest.mark.parametrize("m,k,n", [(1, 5120, 34816), (2, 5120, 34816), (4, 5120, 34816), (3, 4096, 34848),
-                                   (4, 17408, 10240)])
+                                   (4, 17408, 10240), (9, 5120, 34816), (12, 5120, 34816), (16, 5120, 34816),
+                                   (16, 5120, 20480)])
 def test_gate_up_silu_fused_rowsplit(m, k, n):
     x, w, s, b = O.make_inputs(m, k, n, seed=m + 31 * k + n)
     check_gate_up(x, w, s, b)

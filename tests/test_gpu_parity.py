@@ -480,10 +480,25 @@ def test_rowsplit_eight_row_shapes(m, k, n):
         assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
+# 9 to 16 rows beyond the x-in-registers form's reach: the row-split kernel with 16-row fragments,
+# x in LDS in up to 4 K slices (the MLP up projection at 9 and 16 rows: 2 slices; 12 rows over
+# 34816 columns: 4; K = 2048 over 16384 columns: the small form; K = 6144).
+@pytest.mark.parametrize("m,k,n", [(9, 5120, 17408), (16, 5120, 17408), (12, 5120, 34816), (16, 5120, 10240),
+                                   (16, 2048, 16384), (13, 6144, 5120)])
+def test_rowsplit_sixteen_row_shapes(m, k, n):
+    note(f"row-split 16-row {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 23 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split 16-row {m}x{k}x{n}", (x, w, s, b))
+    for _ in range(2):
+        assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
-@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848)])
+@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848), (16, 17408), (12, 34816)])
 def test_rowsplit_small_and_eight_row_one_hot_is_exact_dequant(kind, m, n):
-    """One-hot rows of x through the small form and the 8-row fragments: each output is one
+    """One-hot rows of x through the small form and the 8- and 16-row fragments: each output is one
     dequantized weight, equal to the oracle's bit for bit (fast form, general form, both)."""
     k = 5120
     rng = np.random.default_rng({"fast": 31, "mixed": 32, "slow": 33}[kind] + n + m)
