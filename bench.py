@@ -156,7 +156,9 @@ def time_graph(torch, call, reps: int = 20, replays: int = 5) -> float:
     torch.cuda.current_stream().wait_stream(side)
     torch.cuda.synchronize()
     g = torch.cuda.CUDAGraph()
-    with torch.cuda.graph(g):
+    # Captured on the warmed-up stream: the library's workspaces are per stream, and a call that
+    # would need one to grow during capture is refused.
+    with torch.cuda.graph(g, stream=side):
         st = torch.cuda.current_stream().cuda_stream
         for i in range(reps):
             call(i, st)
@@ -173,18 +175,23 @@ def time_graph(torch, call, reps: int = 20, replays: int = 5) -> float:
 
 def measure_fused(torch, lib, dev, wl: Workload) -> dict:
     """The ops either side of the projection: the fused gate+up with its SiLU·mul epilogue on the c1
-    weights (the gate and up projections stacked), and the residual add + RMS norm at the model
+    weights (the gate and up projections stacked; decode rows and a 16-row verify batch), and the
+    residual add + RMS norm at the model
     width for decode (4 rows) and a prefill chunk (4096 rows). Timed as graph replays of 20
     back-to-back calls on rotating inputs (no host dispatch in the figure). HBM-bound; bytes are the
     algorithmic ones (weights, scales and biases, x, y; for the norm x, r, h, n and the weight row)."""
     out = {}
     n2 = wl.n // 2
-    for m in wl.rows:
+    # Decode rows on the workload's x, and a 16-row tree-verify batch.
+    g16 = torch.Generator(device="cpu").manual_seed(16)
+    x16 = torch.randn(16, wl.k, generator=g16).to(torch.bfloat16).to(dev)
+    for m in (*wl.rows, 16):
         y = torch.empty((m, n2), dtype=torch.int16, device=dev)
+        xm = wl.x if m <= max(wl.rows) else x16
 
-        def call(i, stream, m=m, y=y):
+        def call(i, stream, m=m, y=y, xm=xm):
             c = i % wl.copies
-            rc = lib.qmm4_gate_up_silu_bf16(wl.x.data_ptr(), wl.w[c].data_ptr(), wl.s[c].data_ptr(),
+            rc = lib.qmm4_gate_up_silu_bf16(xm.data_ptr(), wl.w[c].data_ptr(), wl.s[c].data_ptr(),
                                             wl.b[c].data_ptr(), y.data_ptr(), m, wl.n, wl.k, 64, 4, 1, stream)
             if rc != 0:
                 raise RuntimeError(f"qmm4_gate_up_silu_bf16 failed ({rc}): {lib.qmm4_last_error().decode()}")
@@ -252,8 +259,9 @@ def measure_layer_tail(torch, dev, rows_list=(4, 64), n_layers: int = 2, samples
     and c2 down projection shapes), per forward: eager calls from Python against one replay of the
     same layers captured in a HIP graph. Random weights; the same layers for every sample. Up to 4
     rows a layer is 3 kernels (the norm folded into the gate+up, the down projection, the next
-    norm); 64 rows run the norm, the gate+up projection, its SiLU·mul pass, the down projection and
-    its reduce, and the next norm."""
+    norm); 16 rows (a tree-verify batch) run the norm, the gate+up with its epilogue fused, the
+    down projection and its reduce, and the next norm; 64 rows run the norm, the gate+up
+    projection, its SiLU·mul pass, the down projection and its reduce, and the next norm."""
     from mlx_tree_spec_amd import GraphedTail, MLPLayer, QuantizedLinear, QuantizedMLP, stack_tail
 
     d, h = 5120, 17408
@@ -540,7 +548,7 @@ def main() -> int:
     log("[bench] fused ops either side of the projection")
     fused = measure_fused(torch, lib, dev, wl)
     log("[bench] verify-forward layer tails (MLP half), eager and graph-captured")
-    fused["layer_tail"] = measure_layer_tail(torch, dev)
+    fused["layer_tail"] = measure_layer_tail(torch, dev, rows_list=(4, 16, 64))
     # Timed region: exactly K steps, synchronized on both sides.
     for _ in range(args.warmup):
         wl.step()
