@@ -558,7 +558,27 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
     passes = (share + kW * maxb - 1) / (kW * maxb);
     bw = (NB + cus * passes - 1) / (cus * passes);
   }
-  const int id = pick(wide ? (bw + kW - 1) / kW : kRpNarrowBpw);
+  // Narrow: ranges of kRpNarrowBpw or one more block per wave, whichever gives a workgroup the
+  // shorter walk (blocks x phases of its K slice x super-steps per phase) with the grid filling
+  // the CUs; a tie keeps the smaller ranges (fewer partial tiles to add). 17-32 rows over
+  // 5120 -> 17408: 68 ranges x 3 slices (204 workgroups) took 31.0-32.0 us, 46 x 5 (230)
+  // 28.1-28.7 us; 17408 -> 5120 ties and keeps 20 x 12.
+  auto walk = [&](int c) {
+    int cm, cv, cb, items;
+    size_t l;
+    rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
+    const int np = ks / cv;
+    const int ranges = (NB + kW * cb - 1) / (kW * cb);
+    int sp = cus / ranges;
+    if (sp < 1) sp = 1;
+    if (sp > np) sp = np;
+    return (long long)kW * cb * ((np + sp - 1) / sp) * cv;
+  };
+  int id = pick(wide ? (bw + kW - 1) / kW : kRpNarrowBpw);
+  if (!wide && id >= 0) {
+    const int id2 = pick(kRpNarrowBpw + 1);
+    if (id2 >= 0 && id2 != id && walk(id2) < walk(id)) id = id2;
+  }
   if (id < 0) return false;
   int cm, v, bpw, items;
   size_t lds;
