@@ -38,6 +38,7 @@ HBM_PEAK_GBS = 8000.0
 MFMA_BF16_PEAK_TFLOPS = 2500.0
 MALL_BYTES = 256 << 20
 ROTATE_BYTES = 640e6
+WARM_S = 0.25  # seconds of back-to-back calls before a workload is timed
 
 WORKLOADS = {
     # name: (config index, rows, K, N, sigma)
@@ -124,6 +125,7 @@ class Workload:
         self.x = t(x, np.int16)
         self.y = {m: torch.empty((m, n), dtype=torch.int16, device=dev) for m in rows}
         self.lib = lib
+        self.torch = torch
         self.stream = torch.cuda.current_stream(dev).cuda_stream
         self.i = 0
 
@@ -139,6 +141,18 @@ class Workload:
     def step(self) -> None:
         for m in self.rows:
             self.launch(m)
+
+    def warm(self, seconds: float = WARM_S) -> None:
+        """Back-to-back calls at every row count for at least `seconds` of wall time, so that the
+        GPU's clocks have ramped up again after the host built this workload's inputs (the first
+        ~100 ms of work after an idle spell run at lower clocks)."""
+        t0 = time.perf_counter()
+        while True:
+            for _ in range(8):
+                self.step()
+            self.torch.cuda.synchronize()
+            if time.perf_counter() - t0 >= seconds:
+                break
 
     def step_bytes(self) -> int:
         return sum(bytes_per_call(m, self.k, self.n) for m in self.rows)
@@ -318,9 +332,7 @@ def measure_rows(torch, lib, dev, samples: int, table: dict) -> dict:
     out = {}
     for name, spec in table.items():
         wl = Workload(name, torch, lib, dev, spec=spec)
-        for _ in range(2):
-            wl.step()
-        torch.cuda.synchronize()
+        wl.warm()
         for m in wl.rows:
             ts = time_launches(torch, wl, m, samples)
             med = statistics.median(ts)
@@ -341,9 +353,7 @@ def measure_shard8(torch, lib, dev, samples: int) -> dict:
     out = {}
     for name, spec in SHARD8.items():
         wl = Workload(name, torch, lib, dev, spec=spec)
-        for _ in range(2):
-            wl.step()
-        torch.cuda.synchronize()
+        wl.warm()
         for m in wl.rows:
             ts = time_launches(torch, wl, m, samples)
             med = statistics.median(ts)
@@ -512,9 +522,7 @@ def main() -> int:
     for name in only:
         log(f"[bench] {name}: {DESCR[name]}")
         wl = Workload(name, torch, lib, dev)
-        for _ in range(3):
-            wl.step()
-        torch.cuda.synchronize()
+        wl.warm()
         res = {"descr": DESCR[name], "weight_copies": wl.copies, "per_m": {}}
         for m in wl.rows:
             ts = time_launches(torch, wl, m, args.samples)
