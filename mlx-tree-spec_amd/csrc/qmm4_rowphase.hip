@@ -562,8 +562,12 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   // shorter walk (blocks x phases of its K slice x super-steps per phase) with the grid filling
   // the CUs; a tie keeps the smaller ranges (fewer partial tiles to add). 17-32 rows over
   // 5120 -> 17408: 68 ranges x 3 slices (204 workgroups) took 31.0-32.0 us, 46 x 5 (230)
-  // 28.1-28.7 us; 17408 -> 5120 ties and keeps 20 x 12.
-  auto walk = [&](int c) {
+  // 28.1-28.7 us; 17408 -> 5120 ties and keeps 20 x 12. Ranges of one block per wave (twice the
+  // ranges, half the K slices, the same walk) when those ranges would leave a workgroup at most
+  // 3 phases, too few to pipeline: 32 / 64 x 5120 -> 5120 17.0 / 20.6 -> 16.0 / 19.4 us,
+  // 16 / 32 x 17408 -> 5120 24.8 / 27.9 -> 22.6 / 26.5 us; with 6 phases (64 x 17408 -> 5120)
+  // the doubled x reads cost more (33.5 -> 37.2 us).
+  auto narrow = [&](int c, int* phases) {
     int cm, cv, cb, items;
     size_t l;
     rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
@@ -572,12 +576,24 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
     int sp = cus / ranges;
     if (sp < 1) sp = 1;
     if (sp > np) sp = np;
-    return (long long)kW * cb * ((np + sp - 1) / sp) * cv;
+    *phases = (np + sp - 1) / sp;
+    return (long long)kW * cb * *phases * cv;
   };
   int id = pick(wide ? (bw + kW - 1) / kW : kRpNarrowBpw);
   if (!wide && id >= 0) {
+    int ph = 0, ph2 = 0, ph1 = 0;
+    long long walk = narrow(id, &ph);
     const int id2 = pick(kRpNarrowBpw + 1);
-    if (id2 >= 0 && id2 != id && walk(id2) < walk(id)) id = id2;
+    if (id2 >= 0 && id2 != id) {
+      const long long walk2 = narrow(id2, &ph2);
+      if (walk2 < walk) {
+        id = id2;
+        walk = walk2;
+        ph = ph2;
+      }
+    }
+    const int id1 = pick(1);
+    if (id1 >= 0 && id1 != id && ph <= 3 && narrow(id1, &ph1) <= walk) id = id1;
   }
   if (id < 0) return false;
   int cm, v, bpw, items;

@@ -564,9 +564,12 @@ def test_rowsplit_xreg_one_hot_is_exact_dequant(kind):
 # K = 3072 ends in a partial scale window. 65984 columns (the drafter's head) give a workgroup 17
 # blocks (the 3-blocks-per-wave variants), 99984 and 131072 columns 25 and 32 blocks (4 per wave).
 # 24 rows over 5120 -> 17408: K split over ranges of 3 blocks per wave (46 ranges x 5 slices).
+# Ranges of one block per wave where two would leave a workgroup at most 3 phases: 12 x 17408 ->
+# 5120 (40 ranges x 6 slices of 6 phases), 48 x 6144 -> 5120 (4 phases), 32 x 2048 -> 8192.
 @pytest.mark.parametrize("m,k,n", [(17, 5120, 4096), (33, 2048, 32784), (8, 5120, 34848), (48, 3072, 33024),
                                    (64, 1024, 2064), (24, 17408, 1024), (16, 5120, 65984), (32, 2048, 65984),
-                                   (16, 5120, 99984), (32, 2048, 131072), (24, 5120, 17408)])
+                                   (16, 5120, 99984), (32, 2048, 131072), (24, 5120, 17408), (12, 17408, 5120),
+                                   (48, 6144, 5120), (32, 2048, 8192)])
 def test_rowphase_shapes(m, k, n):
     note(f"row-phase {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, seed=m * 11 + k + n)
