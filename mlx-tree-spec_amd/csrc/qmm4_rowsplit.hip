@@ -134,11 +134,12 @@ __host__ __device__ inline size_t rowsplit_red_offset(int Kp, int MP, int units,
 // then the 4 waves in order), so the staged rows are the bits that kernel would store for n, and y
 // is the bits of the unfused pair. Each workgroup reads all of x and r (from L2 after the first),
 // stages its K slice of n, and workgroup 0 writes h and n.
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM>
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "x rows per fragment");
   static_assert(!SMALL || (!FUSED && !KSPLIT), "small plans are plain whole-K projections");
+  static_assert(!PAIR || (!FUSED && !KSPLIT && !SMALL && !NORM), "paired units are plain whole-K projections");
   static_assert(!NORM || (MP == 4 && kRsThreads == MP * kRsNormThreads), "one thread group per normalised row");
   constexpr int G = MP / 4;  // lane groups holding output rows
   typedef f32x4 RowSums[G];  // the sums of one output column over x rows 4 g + r
@@ -146,10 +147,13 @@ void rowsplit_kernel(RowSplitParams P) {
   const int S = P.Kp >> 7;  // super-steps per row in this workgroup's K slice
   const int SU = P.SU;
   const int U = P.RB * SU;
+  // PAIR: a wave takes units 2p and 2p + 1 (consecutive steps of one block; SU is even) together
+  // and leaves their sum in one slot, so a block has SU / 2 slots.
+  const int SS = PAIR ? SU / 2 : SU;
   u32x4* xs = reinterpret_cast<u32x4*>(lds);
   // SMALL: the slots take over the x area once x is dead.
   f32x4* part = reinterpret_cast<f32x4*>(lds + (SMALL ? 0 : rowsplit_xs_bytes(P.Kp, MP)));
-  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.Kp, MP) + rowsplit_part_bytes(U, MP));
+  u32x4* spare = reinterpret_cast<u32x4*>(lds + rowsplit_xs_bytes(P.Kp, MP) + rowsplit_part_bytes(P.RB * SS, MP));
   int* next = reinterpret_cast<int*>(spare + 1);
 
   const int tid = threadIdx.x;
@@ -282,7 +286,9 @@ void rowsplit_kernel(RowSplitParams P) {
   // Whole K: the ring's first fetches go out behind the x loads, before their stores. K slices
   // (few units per workgroup): the x stores first, then the fetches (measured: the decode down
   // projection M = 1 over 5120 x 17408 21.4 -> 20.1 us; with whole K, 27.4 -> 28.4 us the other way).
-  int ua = wave, ub = wave + kRsWaves;
+  int ua = PAIR ? 2 * wave : wave, ub = PAIR ? 2 * wave + 1 : wave + kRsWaves;
+  // Units (pairs) handed out by the LDS counter after the ring's first fill.
+  constexpr int kFirst = PAIR ? kRsWaves : kRsPF * kRsWaves;
   if constexpr (!KSPLIT) {
     fetch(0, ua);
     fetch(1, ub);
@@ -320,7 +326,7 @@ void rowsplit_kernel(RowSplitParams P) {
       }
     }
     if constexpr (!SMALL) {
-      if (tid == 0) *next = kRsPF * kRsWaves;
+      if (tid == 0) *next = kFirst;
     }
   } else if constexpr (SMALL) {
     // The weights (from HBM, the longest latency) went out first; x follows from L2. Every wave
@@ -329,7 +335,7 @@ void rowsplit_kernel(RowSplitParams P) {
     asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
   } else {
     store_x(nxb - 1);
-    if (tid == 0) *next = kRsPF * kRsWaves;
+    if (tid == 0) *next = kFirst;
   }
   __syncthreads();
   if constexpr (KSPLIT) {
@@ -342,10 +348,9 @@ void rowsplit_kernel(RowSplitParams P) {
   int ndone = 0;
   __builtin_amdgcn_s_setprio(3);
 
-  auto compute = [&](int j, int st, auto fast) __attribute__((always_inline)) {
+  auto compute = [&](int j, int st, auto fast, f32x4 acc) __attribute__((always_inline)) {
     constexpr bool FAST = decltype(fast)::value;
     const u32x4* xb = xs + (size_t)st * V * 16 * MP;
-    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
     for (int v = 0; v < V; ++v) {
       const int e2 = 2 * v + (g >> 1);
@@ -378,11 +383,12 @@ void rowsplit_kernel(RowSplitParams P) {
       const int e2 = 2 * v + (g >> 1);
       bad |= !fast_scale_ok((sv[j].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
     }
+    const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
     f32x4 acc;
     if (__builtin_amdgcn_ballot_w64(bad) == 0)
-      acc = compute(j, st, std::true_type{});
+      acc = compute(j, st, std::true_type{}, zero);
     else
-      acc = compute(j, st, std::false_type{});
+      acc = compute(j, st, std::false_type{}, zero);
     if (g < G) part[(u * G + g) * 16 + n] = acc;
     ++ndone;
     // A wave's issue priority falls with the units it has done: the SIMD arbiter otherwise
@@ -406,8 +412,9 @@ void rowsplit_kernel(RowSplitParams P) {
         const int e2 = 2 * v + (g >> 1);
         bad |= !fast_scale_ok((sv[j].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
       }
-      if (__builtin_amdgcn_ballot_w64(bad) == 0) return compute(j, st, std::true_type{});
-      return compute(j, st, std::false_type{});
+      const f32x4 zero = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (__builtin_amdgcn_ballot_w64(bad) == 0) return compute(j, st, std::true_type{}, zero);
+      return compute(j, st, std::false_type{}, zero);
     };
     f32x4 acc0 = {0.0f, 0.0f, 0.0f, 0.0f}, acc1 = acc0;
     if (ua < U) acc0 = unit_sums(ua, std::integral_constant<int, 0>{});
@@ -416,6 +423,37 @@ void rowsplit_kernel(RowSplitParams P) {
     if (g < G) {
       if (ua < U) part[(ua * G + g) * 16 + n] = acc0;
       if (ub < U) part[(ub * G + g) * 16 + n] = acc1;
+    }
+  } else if constexpr (PAIR) {
+    // Half 0 of the pair from slot 0, slot 0 refilled with the next pair's half 0, half 1 from
+    // slot 1 added to the same sums, slot 1 refilled with the next pair's half 1.
+    auto half = [&](int u, auto jc, f32x4 acc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      const int st = u - (u / SU) * SU;
+      bool bad = false;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int e2 = 2 * v + (g >> 1);
+        bad |= !fast_scale_ok((sv[j].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
+      }
+      if (__builtin_amdgcn_ballot_w64(bad) == 0) return compute(j, st, std::true_type{}, acc);
+      return compute(j, st, std::false_type{}, acc);
+    };
+    while (ua < U) {
+      int taken = 0;
+      if (lane == 0) taken = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+      const int np = __builtin_amdgcn_readfirstlane(taken);
+      f32x4 acc = half(ua, std::integral_constant<int, 0>{}, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+      fetch(0, 2 * np);
+      acc = half(ub, std::integral_constant<int, 1>{}, acc);
+      if (g < G) part[((ua >> 1) * G + g) * 16 + n] = acc;
+      ++ndone;
+      if (ndone == 1) __builtin_amdgcn_s_setprio(2);
+      else if (ndone == 2) __builtin_amdgcn_s_setprio(1);
+      else if (ndone == 3) __builtin_amdgcn_s_setprio(0);
+      fetch(1, 2 * np + 1);
+      ua = 2 * np;
+      ub = ua + 1;
     }
   } else {
     for (;;) {
@@ -436,10 +474,10 @@ void rowsplit_kernel(RowSplitParams P) {
     const int b = lrow >> 4, nn = lrow & 15;
 #pragma unroll
     for (int gg = 0; gg < G; ++gg) sum[gg] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int st = 0; st < SU; ++st) {
+    for (int st = 0; st < SS; ++st) {
 #pragma unroll
       for (int gg = 0; gg < G; ++gg) {
-        const f32x4 c = part[((b * SU + st) * G + gg) * 16 + nn];
+        const f32x4 c = part[((b * SS + st) * G + gg) * 16 + nn];
         sum[gg][0] += c[0]; sum[gg][1] += c[1]; sum[gg][2] += c[2]; sum[gg][3] += c[3];
       }
     }
@@ -663,6 +701,7 @@ bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
   plan->MP = 16;
   plan->small = true;
   plan->xreg = true;
+  plan->pair = false;
   plan->V = kXrV;
   plan->fused = false;
   plan->Nout = N;
@@ -706,6 +745,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       plan->MP = MP;
       plan->small = true;
       plan->xreg = false;
+      plan->pair = false;
       plan->V = 4;
       plan->fused = false;
       plan->Nout = nout;
@@ -737,12 +777,24 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
     const int RB = ((fused ? 2 * R : R) + 15) / 16;
     const int SU = S / V;
     if (MP == 4 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
-    const size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
+    size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
+    // Whole K whose unit slots do not fit: paired units (one slot per two steps of a block)
+    // before K slices, e.g. the 248320-column vocabulary head at 1-4 rows (61 blocks x 10 steps
+    // per CU) or the 65984-column head at 5-8 rows.
+    bool pair = false;
+    if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && SU % 2 == 0) {
+      const size_t ps = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU / 2, MP) + 32;
+      if (ps <= 160 * 1024) {
+        smem = ps;
+        pair = true;
+      }
+    }
     if (smem > 160 * 1024) continue;
     const int ranges = (nout + R - 1) / R;
     plan->MP = MP;
     plan->small = false;
     plan->xreg = false;
+    plan->pair = pair;
     plan->V = V;
     plan->fused = fused;
     plan->Nout = nout;
@@ -767,18 +819,18 @@ size_t rowsplit_smem(const RowSplitPlan& plan, bool norm) {
                                  sizeof(float) * (kRsThreads / 64));
 }
 
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM>
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false>
 hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM>),
+        reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM, PAIR>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRsLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM>), dim3(plan.blocks), dim3(kRsThreads),
-                     rowsplit_smem(plan, NORM), stream, P);
+  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM, PAIR>), dim3(plan.blocks),
+                     dim3(kRsThreads), rowsplit_smem(plan, NORM), stream, P);
   return hipGetLastError();
 }
 
@@ -791,6 +843,9 @@ hipError_t launch_rowsplit_k(const RowSplitPlan& plan, const RowSplitParams& P, 
 template <int MP, bool NORM>
 hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true, NORM>(plan, P, stream);
+  if constexpr (!NORM) {
+    if (plan.pair) return launch_rowsplit_t<MP, 4, false, false, false, false, true>(plan, P, stream);
+  }
   if (plan.fused)
     return plan.V == 5 ? launch_rowsplit_k<MP, 5, true, NORM>(plan, P, stream)
                        : launch_rowsplit_k<MP, 4, true, NORM>(plan, P, stream);
@@ -804,7 +859,7 @@ hipError_t launch_rowsplit_xreg(const RowSplitPlan& plan, const RowSplitParams& 
 }
 
 bool rowsplit_norm_ok(const RowSplitPlan& plan, int M, int K) {
-  return !plan.xreg && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
+  return !plan.xreg && !plan.pair && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
          K <= kRsNormThreads * kRsNormChunks * 8 && rowsplit_smem(plan, true) <= kRsLds;
 }
 

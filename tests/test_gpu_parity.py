@@ -319,7 +319,7 @@ MODEL_LINEARS = [(5120, 17408), (17408, 5120), (5120, 10240), (5120, 6144), (614
 
 
 @pytest.mark.parametrize("k,n,rows", [(k, n, (1, 4, 16, 48, 64, 128, 512)) for k, n in MODEL_LINEARS]
-                         + [(5120, 248320, (1, 4, 16, 32)), (5120, 65984, (1, 4, 16, 32, 64))],
+                         + [(5120, 248320, (1, 4, 16, 32)), (5120, 65984, (1, 4, 6, 16, 32, 64))],
                          ids=lambda v: str(v) if not isinstance(v, tuple) else "rows")
 def test_model_linear_shapes(k, n, rows):
     x, w, s, b = O.make_inputs(max(rows), k, n, seed=k + n)
@@ -495,11 +495,28 @@ def test_rowsplit_sixteen_row_shapes(m, k, n):
         assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
+# Whole K with units taken in pairs (two consecutive steps of a block summed into one LDS slot)
+# where one slot per step does not fit: 1-4 rows over the 248320-column vocabulary head (61 blocks
+# x 10 steps per CU; N = 248336 leaves a partial last range), 6 rows over the 65984-column head
+# (8-row fragments), 2 rows at K = 4096 (8 steps per block).
+@pytest.mark.parametrize("m,k,n", [(3, 5120, 248336), (6, 5120, 65984), (2, 4096, 262144)])
+def test_rowsplit_paired_units(m, k, n):
+    note(f"row-split paired units {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 29 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split paired units {m}x{k}x{n}", (x, w, s, b))
+    for _ in range(2):
+        assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
-@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848), (16, 17408), (12, 34816)])
+@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848), (16, 17408), (12, 34816), (2, 248320),
+                                 (6, 65984)])
 def test_rowsplit_small_and_eight_row_one_hot_is_exact_dequant(kind, m, n):
-    """One-hot rows of x through the small form and the 8- and 16-row fragments: each output is one
-    dequantized weight, equal to the oracle's bit for bit (fast form, general form, both)."""
+    """One-hot rows of x through the small form, the 8- and 16-row fragments and paired units: each
+    output is one dequantized weight, equal to the oracle's bit for bit (fast form, general form,
+    both)."""
     k = 5120
     rng = np.random.default_rng({"fast": 31, "mixed": 32, "slow": 33}[kind] + n + m)
     s, b = scale_bias_pairs(kind, n * (k // 64), rng)
