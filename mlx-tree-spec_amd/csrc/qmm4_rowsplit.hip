@@ -764,7 +764,11 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
   // 9 to 16 rows: at most 4 K slices (x slices of 16 rows are large; with 8 slices, e.g. the
   // 65984-column head, the cross-workgroup merge of the slices costs more than it saves).
   const int max_ks = MP == 8 ? 8 : 4;
-  for (int ks = 1; ks <= max_ks; ks *= 2) {
+  // A second pass takes whole K for up to 4 rows even with fewer than 4 row blocks per CU, when
+  // no K split leaves each workgroup 3 units per wave (measured: 12288 -> 5120 at 1 row, 21.5 us
+  // on the stream-K skinny kernel, 17.0 us so).
+  for (int pass = 0; pass < 2; ++pass)
+  for (int ks = 1; ks <= (pass == 0 ? max_ks : 1); ks *= 2) {
     if (K % (128 * ks) != 0) continue;
     const int kp = K / ks;
     const int S = kp >> 7;
@@ -776,7 +780,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
     const int R = ((nout + target - 1) / target + 3) / 4 * 4;
     const int RB = ((fused ? 2 * R : R) + 15) / 16;
     const int SU = S / V;
-    if (MP == 4 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
+    if (MP == 4 && pass == 0 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
     size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
     // Whole K whose unit slots do not fit: paired units (one slot per two steps of a block)
     // before K slices, e.g. the 248320-column vocabulary head at 1-4 rows (61 blocks x 10 steps

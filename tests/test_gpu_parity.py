@@ -405,6 +405,19 @@ def test_rowsplit_k_slices(m, k, n):
         assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
+# Up to 4 rows where no K split leaves every workgroup 3 units per wave and the columns give a CU
+# fewer than 4 row blocks (12288 -> 5120: 2 blocks, 24 steps): whole K all the same.
+@pytest.mark.parametrize("m", [1, 4])
+def test_rowsplit_whole_k_fallback(m):
+    k, n = 12288, 5120
+    note(f"row-split whole-K fallback {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 31 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split whole-K fallback {m}x{k}x{n}", (x, w, s, b))
+    assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 def test_rowsplit_k_slices_one_hot_is_exact_dequant():
     """One-hot rows in the first and the second K slice: each output is one dequantized weight."""
     n, k, m = 5120, 17408, 4
