@@ -13,7 +13,7 @@
 // row pitch keeps the 16-byte fragment reads free of bank conflicts.
 //
 // Pipeline: the raw inputs of a K step (activation chunks, packed codes) are loaded into registers
-// two steps ahead of their use, through buffer resources (rows past M and columns past N read as
+// two steps ahead of their use (four in the stream-K launches), through buffer resources (rows past M and columns past N read as
 // zero); scales and biases come 8 groups per 16-byte load when K % 512 == 0. While the MFMAs of
 // step kt run from LDS stage kt % 2, the waves write step kt + 1 into the other stage: activations
 // as loaded, weights dequantized exactly in registers (dequant_word_fast; a thread whose group has
@@ -26,8 +26,9 @@
 //    tiles are walked in groups of 4 row tiles, so a group shares weight and activation blocks in
 //    L2.
 //  * At most one 128 x 128 tile per CU (65-256 rows of the model's projections): stream-K over
-//    128 x 128 tiles. The tiles x K units are split evenly over every resident workgroup (two per
-//    CU); a workgroup's first and last segments may cover part of a tile and leave fp32 partial
+//    128 x 128 tiles. The tiles x K units are split evenly over every resident workgroup (one per
+//    CU, with a 4-step register ring when K % 512 == 0: 65-128 rows 2-6% faster than two per CU
+//    with a 2-step ring); a workgroup's first and last segments may cover part of a tile and leave fp32 partial
 //    tiles, which gemm_sk_reduce_kernel adds in K order (the same bits whichever workgroup ran a
 //    segment).
 // The output tile is staged through LDS and stored as 16-byte row chunks.
@@ -46,6 +47,7 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kWavesN = kWaves / 2;
 constexpr int kGroupM = 4;
 constexpr int kTile = 256;            // the grid's tile; tail launches cut a tile into 128 x 128 quarters
+constexpr int kSkRing = 4;            // K steps of raw inputs in registers, stream-K launches with SB8
 
 struct GemmParams {
   const uint16_t* x;
@@ -119,10 +121,14 @@ __device__ __forceinline__ void part_item_coords(int e, int* m, int* n) {
 
 // SB8: scales and biases are loaded 8 groups (8 K steps) at a time with one 16-byte load per
 // column (K % 512 == 0); otherwise one 2-byte load per K step.
-// The 128 x 128 configuration is held to 128 VGPRs so that two workgroups share a CU.
-template <int BM, int BN, bool SB8>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 128 ? 4 : 2)))
+// D: K steps of raw inputs held in registers (a ring; step kt + D is loaded as step kt is written
+// out). The 128 x 128 configuration with D = 2 is held to 128 VGPRs so that two workgroups share a
+// CU (the quarter tiles of full-tile launches); stream-K launches with SB8 use D = 4 at one
+// workgroup per CU.
+template <int BM, int BN, bool SB8, int D = 2>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 128 && D == 2 ? 4 : 2)))
 void gemm_kernel(GemmParams P) {
+  static_assert(D == 2 || (SB8 && D == 4), "raw ring depth: its index must be static in the loop unrolled by 8");
   using C = GemmCfg<BM, BN>;
   constexpr int I = C::I, J = C::J, AJ = C::AJ, WPT = C::WPT, LDC = C::LDC;
   extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
@@ -190,7 +196,7 @@ void gemm_kernel(GemmParams P) {
     const uint32_t woff = col * (uint32_t)(P.K >> 1) + (uint32_t)(b_part * WPT * 4);
     const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
 
-    Raw<C> raw[2];
+    Raw<C> raw[D];
     // Steps past the segment's last are clamped to it (their data is written to an LDS stage
     // nobody reads).
     auto load = [&](int kt, Raw<C>& R) {
@@ -275,7 +281,7 @@ void gemm_kernel(GemmParams P) {
     auto step = [&](int kt, auto parity, auto ucst) {
       constexpr int ST = decltype(parity)::value;
       constexpr int U = decltype(ucst)::value;  // SB8: kt % 8 (the loop is unrolled by 8)
-      Raw<C>& R = raw[ST ^ 1];
+      Raw<C>& R = raw[D == 2 ? (ST ^ 1) : (U + 1) % D];
       uint32_t sbits, bbits;
       if constexpr (SB8) {
         // Step kt + 1's group: of the current block, or the first of the next one (step 7).
@@ -313,17 +319,17 @@ void gemm_kernel(GemmParams P) {
       }
       if (!fast_scale_ok(sbits)) store_b_exact(R, ST ^ 1, sbits, bbits);
       __syncthreads();
-      load(kt + 3, R);
+      load(kt + 1 + D, R);
       if constexpr (SB8)
-        if constexpr (U == 5) load_sb8(kt + 3, snext, bnext);  // the next block, first used at step 7
+        if constexpr (U == (D == 2 ? 5 : 1)) load_sb8(kt + (D == 2 ? 3 : 7), snext, bnext);  // the next block, first used at step 7
       // Keep these loads right behind the barrier (the scheduler would sink them toward their use
       // two steps later, into the middle of the next step's MFMAs).
       __builtin_amdgcn_sched_barrier(0);
     };
 
-    // Prologue: steps kb and kb + 1 in registers, step kb in LDS, step kb + 2 in flight.
-    load(kb, raw[0]);
-    load(kb + 1, raw[1]);
+    // Prologue: steps kb .. kb + D - 1 in registers, step kb in LDS, step kb + D in flight.
+#pragma unroll
+    for (int i = 0; i < D; ++i) load(kb + i, raw[i]);
     if constexpr (SB8) load_sb8(kb, scur, bcur);
     {
       uint32_t sbits, bbits;
@@ -332,7 +338,7 @@ void gemm_kernel(GemmParams P) {
       store_b_fast(raw[0], 0, 0, WPT, sbits, bbits);
       if (!fast_scale_ok(sbits)) store_b_exact(raw[0], 0, sbits, bbits);
     }
-    load(kb + 2, raw[0]);
+    load(kb + D, raw[0]);
     __syncthreads();
 
     auto two = [&](int kt, auto u0) __attribute__((always_inline)) {
@@ -473,17 +479,17 @@ __global__ __launch_bounds__(kSkRedThreads) void gemm_sk_reduce_kernel(GemmParam
   }
 }
 
-template <int BM, int BN, bool SB8>
+template <int BM, int BN, bool SB8, int D = 2>
 hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
   constexpr size_t smem = GemmCfg<BM, BN>::kSmem;
   static bool attr_set = false;  // the attribute is per function; setting it twice is harmless
   if (!attr_set) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, SB8>),
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_kernel<BM, BN, SB8, D>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((gemm_kernel<BM, BN, SB8>), dim3(blocks), dim3(kThreads), smem, stream, P);
+  hipLaunchKernelGGL((gemm_kernel<BM, BN, SB8, D>), dim3(blocks), dim3(kThreads), smem, stream, P);
   return hipGetLastError();
 }
 
@@ -500,7 +506,7 @@ int sk_occupancy(bool sb8) {
   static int occ[2] = {0, 0};
   int& o = occ[sb8 ? 1 : 0];
   if (o == 0) {
-    const void* f = sb8 ? reinterpret_cast<const void*>(&gemm_kernel<128, 128, true>)
+    const void* f = sb8 ? reinterpret_cast<const void*>(&gemm_kernel<128, 128, true, kSkRing>)
                         : reinterpret_cast<const void*>(&gemm_kernel<128, 128, false>);
     constexpr size_t smem = GemmCfg<128, 128>::kSmem;
     int nb = 0;
@@ -565,7 +571,8 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
     P.ups = sb8 ? 8 : 2;
     P.upt = K / BK / P.ups;
     P.U = (long long)P.tiles_m * P.tiles_n * P.upt;
-    hipError_t e = sb8 ? launch_tiles<128, 128, true>(P, plan.G, stream) : launch_tiles<128, 128, false>(P, plan.G, stream);
+    hipError_t e = sb8 ? launch_tiles<128, 128, true, kSkRing>(P, plan.G, stream)
+                       : launch_tiles<128, 128, false>(P, plan.G, stream);
     if (e != hipSuccess) return e;
     return launch_sk_reduce<128, 128>(P, plan.G, stream);
   }
