@@ -1,4 +1,4 @@
-// Row-split kernel for up to 8 rows of x and many output columns: y = x @ dequant(w)^T.
+// Row-split kernel for up to 16 rows of x and many output columns: y = x @ dequant(w)^T.
 //
 // Same arithmetic and operand layout as the skinny kernel (qmm4_skinny.hip; replaces the
 // reference's qmv_packed and 8-row NAX kernels for decode and small verify batches,
@@ -33,6 +33,10 @@
 //  * Small problems (every unit fits the waves' rings at once, all of x fits LDS): the SMALL form
 //    fetches every unit at the start, loads x straight into LDS behind those fetches, and keeps
 //    each wave's two unit sums in registers until x is dead; the slots then take the x area.
+//  * Whole K over a large N whose slots do not fit (vocabulary heads): PAIR takes units two at a
+//    time (consecutive steps of one block, one slot per pair); OWN (5-16 rows, x alone filling up
+//    to all of LDS) gives wave w blocks w, w + 16, ... whole, their sums kept in registers and
+//    stored to y as each block's last step is done.
 //  * Fused gate+up (FUSED): w is [w_gate; w_up] (N rows, up rows from N / 2), y is [M, N / 2] =
 //    silu(x @ w_gate^T) * (x @ w_up^T). Workgroup p owns output columns [p R, p R + R); its 2R
 //    weight rows are listed gate rows first, then the up rows of the same columns (N / 2 further),
@@ -134,12 +138,13 @@ __host__ __device__ inline size_t rowsplit_red_offset(int Kp, int MP, int units,
 // then the 4 waves in order), so the staged rows are the bits that kernel would store for n, and y
 // is the bits of the unfused pair. Each workgroup reads all of x and r (from L2 after the first),
 // stages its K slice of n, and workgroup 0 writes h and n.
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false>
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false, bool OWN = false>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "x rows per fragment");
   static_assert(!SMALL || (!FUSED && !KSPLIT), "small plans are plain whole-K projections");
   static_assert(!PAIR || (!FUSED && !KSPLIT && !SMALL && !NORM), "paired units are plain whole-K projections");
+  static_assert(!OWN || (!FUSED && !KSPLIT && !SMALL && !NORM && !PAIR && V == 4), "own blocks: plain whole-K projections");
   static_assert(!NORM || (MP == 4 && kRsThreads == MP * kRsNormThreads), "one thread group per normalised row");
   constexpr int G = MP / 4;  // lane groups holding output rows
   typedef f32x4 RowSums[G];  // the sums of one output column over x rows 4 g + r
@@ -216,7 +221,7 @@ void rowsplit_kernel(RowSplitParams P) {
       }
     }
   };
-  if constexpr (!SMALL && !NORM) {
+  if constexpr (!SMALL && !NORM && !OWN) {
     for (int bt = 0; bt + 1 < nxb; ++bt) {
       load_x(bt);
       store_x(bt);
@@ -286,7 +291,14 @@ void rowsplit_kernel(RowSplitParams P) {
   // Whole K: the ring's first fetches go out behind the x loads, before their stores. K slices
   // (few units per workgroup): the x stores first, then the fetches (measured: the decode down
   // projection M = 1 over 5120 x 17408 21.4 -> 20.1 us; with whole K, 27.4 -> 28.4 us the other way).
+  // OWN: wave w takes the SU steps of blocks w, w + 16, ... in turn; q counts its units.
+  const int own_nq = OWN && wave < P.RB ? (P.RB - wave + kRsWaves - 1) / kRsWaves * SU : 0;
+  auto own_unit = [&](int q) { return q < own_nq ? (wave + kRsWaves * (q / SU)) * SU + q % SU : U; };
   int ua = PAIR ? 2 * wave : wave, ub = PAIR ? 2 * wave + 1 : wave + kRsWaves;
+  if constexpr (OWN) {
+    ua = own_unit(0);
+    ub = own_unit(1);
+  }
   // Units (pairs) handed out by the LDS counter after the ring's first fill.
   constexpr int kFirst = PAIR ? kRsWaves : kRsPF * kRsWaves;
   if constexpr (!KSPLIT) {
@@ -328,7 +340,7 @@ void rowsplit_kernel(RowSplitParams P) {
     if constexpr (!SMALL) {
       if (tid == 0) *next = kFirst;
     }
-  } else if constexpr (SMALL) {
+  } else if constexpr (SMALL || OWN) {
     // The weights (from HBM, the longest latency) went out first; x follows from L2. Every wave
     // waits for all of its loads, then the barrier publishes x.
     dma_x_all();
@@ -424,6 +436,52 @@ void rowsplit_kernel(RowSplitParams P) {
       if (ua < U) part[(ua * G + g) * 16 + n] = acc0;
       if (ub < U) part[(ub * G + g) * 16 + n] = acc1;
     }
+  } else if constexpr (OWN) {
+    // Unit q from slot q % 2 into the sums of its block, the slot refilled with unit q + 2; after
+    // a block's last step its 16 columns go straight to y (lane (n, g) holds rows 4 g .. 4 g + 3 of
+    // column n), so nothing but x uses LDS and no barrier follows the first.
+    const __amdgpu_buffer_rsrc_t ryo = __builtin_amdgcn_make_buffer_rsrc(
+        P.y, 0, rsrc_bytes((unsigned long long)P.M * P.Nout * 2), kBufferRsrcWord3);
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    auto step = [&](int q, int& u, auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      const int b = u / SU, st = u - b * SU;
+      bool bad = false;
+#pragma unroll
+      for (int v = 0; v < V; ++v) {
+        const int e2 = 2 * v + (g >> 1);
+        bad |= !fast_scale_ok((sv[j].d[e2 >> 1] >> (16 * (e2 & 1))) & 0xFFFFu);
+      }
+      if (__builtin_amdgcn_ballot_w64(bad) == 0)
+        acc = compute(j, st, std::true_type{}, acc);
+      else
+        acc = compute(j, st, std::false_type{}, acc);
+      u = own_unit(q + 2);
+      fetch(j, u);
+      if (st == SU - 1) {
+        const int col = r0 + b * 16 + n;
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const int m = 4 * g + r;
+          if (m < P.M && col < r1)
+            __builtin_amdgcn_raw_buffer_store_b16((uint16_t)bf16_rne(acc[r]), ryo,
+                                                  (uint32_t)(m * P.Nout + col) * 2u, 0, 0);
+        }
+        acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        // Issue priority falls with the blocks done (as with units taken from the counter).
+        ++ndone;
+        if (ndone == 1) __builtin_amdgcn_s_setprio(2);
+        else if (ndone == 2) __builtin_amdgcn_s_setprio(1);
+        else if (ndone == 3) __builtin_amdgcn_s_setprio(0);
+      }
+    };
+    int q = 0;
+    for (; q + 1 < own_nq; q += 2) {
+      step(q, ua, std::integral_constant<int, 0>{});
+      step(q + 1, ub, std::integral_constant<int, 1>{});
+    }
+    if (q < own_nq) step(q, ua, std::integral_constant<int, 0>{});
+    return;
   } else if constexpr (PAIR) {
     // Half 0 of the pair from slot 0, slot 0 refilled with the next pair's half 0, half 1 from
     // slot 1 added to the same sums, slot 1 refilled with the next pair's half 1.
@@ -702,6 +760,7 @@ bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
   plan->small = true;
   plan->xreg = true;
   plan->pair = false;
+  plan->own = false;
   plan->V = kXrV;
   plan->fused = false;
   plan->Nout = N;
@@ -746,6 +805,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       plan->small = true;
       plan->xreg = false;
       plan->pair = false;
+      plan->own = false;
       plan->V = 4;
       plan->fused = false;
       plan->Nout = nout;
@@ -793,12 +853,22 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
         pair = true;
       }
     }
+    // Neither fits, but all of x does and a CU has at least two blocks per wave: each wave takes
+    // whole blocks (all SU steps) and keeps their sums in registers (no slots), e.g. the
+    // 248320-column vocabulary head at 5-16 rows (61 blocks per CU).
+    bool own = false;
+    if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && RB >= 2 * kRsWaves &&
+        (size_t)S * 16 * MP <= (size_t)kRsSmallXP * kRsThreads && rowsplit_xs_bytes(kp, MP) <= kRsLds) {
+      smem = rowsplit_xs_bytes(kp, MP);
+      own = true;
+    }
     if (smem > 160 * 1024) continue;
     const int ranges = (nout + R - 1) / R;
     plan->MP = MP;
     plan->small = false;
     plan->xreg = false;
     plan->pair = pair;
+    plan->own = own;
     plan->V = V;
     plan->fused = fused;
     plan->Nout = nout;
@@ -823,17 +893,17 @@ size_t rowsplit_smem(const RowSplitPlan& plan, bool norm) {
                                  sizeof(float) * (kRsThreads / 64));
 }
 
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false>
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false, bool OWN = false>
 hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
     hipError_t e = hipFuncSetAttribute(
-        reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM, PAIR>),
+        reinterpret_cast<const void*>(&rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM, PAIR, OWN>),
         hipFuncAttributeMaxDynamicSharedMemorySize, (int)kRsLds);
     if (e != hipSuccess) return e;
     attr_set = true;
   }
-  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM, PAIR>), dim3(plan.blocks),
+  hipLaunchKernelGGL((rowsplit_kernel<MP, V, FUSED, KSPLIT, SMALL, NORM, PAIR, OWN>), dim3(plan.blocks),
                      dim3(kRsThreads), rowsplit_smem(plan, NORM), stream, P);
   return hipGetLastError();
 }
@@ -849,6 +919,7 @@ hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, 
   if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true, NORM>(plan, P, stream);
   if constexpr (!NORM) {
     if (plan.pair) return launch_rowsplit_t<MP, 4, false, false, false, false, true>(plan, P, stream);
+    if (plan.own) return launch_rowsplit_t<MP, 4, false, false, false, false, false, true>(plan, P, stream);
   }
   if (plan.fused)
     return plan.V == 5 ? launch_rowsplit_k<MP, 5, true, NORM>(plan, P, stream)
@@ -863,7 +934,7 @@ hipError_t launch_rowsplit_xreg(const RowSplitPlan& plan, const RowSplitParams& 
 }
 
 bool rowsplit_norm_ok(const RowSplitPlan& plan, int M, int K) {
-  return !plan.xreg && !plan.pair && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
+  return !plan.xreg && !plan.pair && !plan.own && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
          K <= kRsNormThreads * kRsNormChunks * 8 && rowsplit_smem(plan, true) <= kRsLds;
 }
 

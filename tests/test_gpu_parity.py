@@ -523,13 +523,28 @@ def test_rowsplit_paired_units(m, k, n):
         assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
+# Whole K where neither one slot per step nor per pair fits but all of x does, with at least two
+# blocks per wave: each wave owns whole blocks and keeps their sums in registers. 5-16 rows over
+# the 248320-column vocabulary head (61 blocks per CU; 16 rows fill all 160 KB of LDS with x),
+# N = 248336 (a partial last range), 12 rows over the 151936-column head, K = 4096.
+@pytest.mark.parametrize("m,k,n", [(16, 5120, 248336), (5, 5120, 248320), (12, 5120, 151936), (9, 4096, 262144)])
+def test_rowsplit_own_blocks(m, k, n):
+    note(f"row-split own blocks {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 37 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-split own blocks {m}x{k}x{n}", (x, w, s, b))
+    for _ in range(2):
+        assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 @pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848), (16, 17408), (12, 34816), (2, 248320),
-                                 (6, 65984)])
+                                 (6, 65984), (16, 248320), (7, 151936)])
 def test_rowsplit_small_and_eight_row_one_hot_is_exact_dequant(kind, m, n):
-    """One-hot rows of x through the small form, the 8- and 16-row fragments and paired units: each
-    output is one dequantized weight, equal to the oracle's bit for bit (fast form, general form,
-    both)."""
+    """One-hot rows of x through the small form, the 8- and 16-row fragments, paired units and
+    waves owning whole blocks: each output is one dequantized weight, equal to the oracle's bit for
+    bit (fast form, general form, both)."""
     k = 5120
     rng = np.random.default_rng({"fast": 31, "mixed": 32, "slow": 33}[kind] + n + m)
     s, b = scale_bias_pairs(kind, n * (k // 64), rng)
