@@ -833,55 +833,59 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
     const int kp = K / ks;
     const int S = kp >> 7;
     // Units of 4 super-steps (256 bytes of a row: two whole 128-byte lines) where K allows: a unit
-    // boundary inside a line splits it between two waves' fetches.
-    const int V = S % 4 == 0 ? 4 : S % 5 == 0 ? 5 : 0;
-    if (V == 0) continue;
-    const int target = std::max(1, cus / ks);
-    const int R = ((nout + target - 1) / target + 3) / 4 * 4;
-    const int RB = ((fused ? 2 * R : R) + 15) / 16;
-    const int SU = S / V;
-    if (MP == 4 && pass == 0 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
-    size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
-    // Whole K whose unit slots do not fit: paired units (one slot per two steps of a block)
-    // before K slices, e.g. the 248320-column vocabulary head at 1-4 rows (61 blocks x 10 steps
-    // per CU) or the 65984-column head at 5-8 rows.
-    bool pair = false;
-    if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && SU % 2 == 0) {
-      const size_t ps = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU / 2, MP) + 32;
-      if (ps <= 160 * 1024) {
-        smem = ps;
-        pair = true;
+    // boundary inside a line splits it between two waves' fetches. Units of 5 where K does not
+    // allow 4, or where the x slice and the 4-step units' slots do not fit: 9-16 rows over the
+    // 34816 x 5120 gate+up then take 2 K slices of 5-step units instead of 4 slices (42.4 -> 35.5 us
+    // at 16 rows, 16-19% at 9-16 rows, plain or fused).
+    for (int V = 4; V <= 5; ++V) {
+      if (S % V != 0) continue;
+      const int target = std::max(1, cus / ks);
+      const int R = ((nout + target - 1) / target + 3) / 4 * 4;
+      const int RB = ((fused ? 2 * R : R) + 15) / 16;
+      const int SU = S / V;
+      if (MP == 4 && pass == 0 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
+      size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
+      // Whole K whose unit slots do not fit: paired units (one slot per two steps of a block)
+      // before K slices, e.g. the 248320-column vocabulary head at 1-4 rows (61 blocks x 10 steps
+      // per CU) or the 65984-column head at 5-8 rows.
+      bool pair = false;
+      if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && SU % 2 == 0) {
+        const size_t ps = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU / 2, MP) + 32;
+        if (ps <= 160 * 1024) {
+          smem = ps;
+          pair = true;
+        }
       }
+      // Neither fits, but all of x does and a CU has at least two blocks per wave: each wave takes
+      // whole blocks (all SU steps) and keeps their sums in registers (no slots), e.g. the
+      // 248320-column vocabulary head at 5-16 rows (61 blocks per CU).
+      bool own = false;
+      if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && RB >= 2 * kRsWaves &&
+          (size_t)S * 16 * MP <= (size_t)kRsSmallXP * kRsThreads && rowsplit_xs_bytes(kp, MP) <= kRsLds) {
+        smem = rowsplit_xs_bytes(kp, MP);
+        own = true;
+      }
+      if (smem > 160 * 1024) continue;
+      const int ranges = (nout + R - 1) / R;
+      plan->MP = MP;
+      plan->small = false;
+      plan->xreg = false;
+      plan->pair = pair;
+      plan->own = own;
+      plan->V = V;
+      plan->fused = fused;
+      plan->Nout = nout;
+      plan->R = R;
+      plan->RB = RB;
+      plan->SU = SU;
+      plan->KS = ks;
+      plan->Kp = kp;
+      plan->ranges = ranges;
+      plan->blocks = ranges * ks;
+      plan->part_bytes = ks > 1 ? (size_t)plan->blocks * (fused ? 2 * R : R) * (MP / 4) * 16 : 0;
+      plan->smem = smem;
+      return true;
     }
-    // Neither fits, but all of x does and a CU has at least two blocks per wave: each wave takes
-    // whole blocks (all SU steps) and keeps their sums in registers (no slots), e.g. the
-    // 248320-column vocabulary head at 5-16 rows (61 blocks per CU).
-    bool own = false;
-    if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && RB >= 2 * kRsWaves &&
-        (size_t)S * 16 * MP <= (size_t)kRsSmallXP * kRsThreads && rowsplit_xs_bytes(kp, MP) <= kRsLds) {
-      smem = rowsplit_xs_bytes(kp, MP);
-      own = true;
-    }
-    if (smem > 160 * 1024) continue;
-    const int ranges = (nout + R - 1) / R;
-    plan->MP = MP;
-    plan->small = false;
-    plan->xreg = false;
-    plan->pair = pair;
-    plan->own = own;
-    plan->V = V;
-    plan->fused = fused;
-    plan->Nout = nout;
-    plan->R = R;
-    plan->RB = RB;
-    plan->SU = SU;
-    plan->KS = ks;
-    plan->Kp = kp;
-    plan->ranges = ranges;
-    plan->blocks = ranges * ks;
-    plan->part_bytes = ks > 1 ? (size_t)plan->blocks * (fused ? 2 * R : R) * (MP / 4) * 16 : 0;
-    plan->smem = smem;
-    return true;
   }
   return false;
 }

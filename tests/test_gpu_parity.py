@@ -495,7 +495,7 @@ def test_rowsplit_eight_row_shapes(m, k, n):
 
 # 9 to 16 rows beyond the x-in-registers form's reach: the row-split kernel with 16-row fragments,
 # x in LDS in up to 4 K slices (the MLP up projection at 9 and 16 rows: 2 slices; 12 rows over
-# 34816 columns: 4; K = 2048 over 16384 columns: the small form; K = 6144).
+# 34816 columns: 2 slices of 5-step units; K = 2048 over 16384 columns: the small form; K = 6144).
 @pytest.mark.parametrize("m,k,n", [(9, 5120, 17408), (16, 5120, 17408), (12, 5120, 34816), (16, 5120, 10240),
                                    (16, 2048, 16384), (13, 6144, 5120)])
 def test_rowsplit_sixteen_row_shapes(m, k, n):
