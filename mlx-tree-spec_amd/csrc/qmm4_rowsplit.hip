@@ -786,13 +786,18 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
   const int MP = rowsplit_mp(M);
   const int nout = fused ? N / 2 : N;
   // Up to 4 rows: whole K per workgroup when the columns alone give every CU at least 4 row
-  // blocks; otherwise K in 2 or 4 slices over as many workgroups per column range, when each
-  // workgroup still has at least 3 units per wave. 5 to 16 rows (a verify batch of up to 16 tree
-  // nodes): the fewest K slices whose x slice and unit slots fit in LDS (up to 8 slices for 8
-  // rows, 4 for 16).
-  // A problem whose units all fit the waves' rings at once, with all of x in LDS: the SMALL form
-  // (every load in flight from the start, no K slices).
-  if (!fused && K % 512 == 0) {
+  // blocks, or when K <= 8192; otherwise K in 2 or 4 slices over as many workgroups per column
+  // range, when each workgroup still has at least 3 units per wave. 5 to 16 rows (a verify batch
+  // of up to 16 tree nodes): the fewest K slices whose x slice and unit slots fit in LDS (up to 8
+  // slices for 8 rows, 4 for 16), starting from 2 for 6 rows or more when x is over a quarter of
+  // a workgroup's weight bytes.
+  // 6 to 8 rows over at most one row block per CU (N <= 16 x CUs), with all units in the waves'
+  // rings at once and all of x in LDS: the SMALL form (every load in flight from the start, no K
+  // slices). Against the other forms (A/B, interleaved rounds): 6 / 8 x 5120 -> 1024 10.6 / 10.9 ->
+  // 10.1 / 10.7 us, while at 1-5 rows, or with 2-3 blocks per CU, whole K or 2 slices of the
+  // regular form were 1-8% faster (e.g. 1 x 5120 -> 10240 15.1 -> 14.2 us, 12 x 5120 -> 10240
+  // 18.5 -> 17.0 us).
+  if (!fused && K % 512 == 0 && M >= 6 && (nout + cus - 1) / cus <= 16) {
     const int S = K >> 7;
     const int R = ((nout + cus - 1) / cus + 3) / 4 * 4;
     const int RB = (R + 15) / 16;
@@ -824,11 +829,14 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
   // 9 to 16 rows: at most 4 K slices (x slices of 16 rows are large; with 8 slices, e.g. the
   // 65984-column head, the cross-workgroup merge of the slices costs more than it saves).
   const int max_ks = MP == 8 ? 8 : 4;
+  const long long xbytes = (long long)M * K * 2;
+  const long long wbytes = (long long)((nout + cus - 1) / cus) * (fused ? 2 : 1) * (K / 2);
+  const int ks0 = (M >= 6 && 4 * xbytes > wbytes && K % 256 == 0) ? 2 : 1;
   // A second pass takes whole K for up to 4 rows even with fewer than 4 row blocks per CU, when
   // no K split leaves each workgroup 3 units per wave (measured: 12288 -> 5120 at 1 row, 21.5 us
   // on the stream-K skinny kernel, 17.0 us so).
   for (int pass = 0; pass < 2; ++pass)
-  for (int ks = 1; ks <= (pass == 0 ? max_ks : 1); ks *= 2) {
+  for (int ks = pass == 0 ? ks0 : 1; ks <= (pass == 0 ? max_ks : 1); ks *= 2) {
     if (K % (128 * ks) != 0) continue;
     const int kp = K / ks;
     const int S = kp >> 7;
@@ -843,7 +851,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       const int R = ((nout + target - 1) / target + 3) / 4 * 4;
       const int RB = ((fused ? 2 * R : R) + 15) / 16;
       const int SU = S / V;
-      if (MP == 4 && pass == 0 && (ks == 1 ? RB < 4 : RB * SU < 3 * kRsWaves)) continue;
+      if (MP == 4 && pass == 0 && (ks == 1 ? RB < 4 && K > 8192 : RB * SU < 3 * kRsWaves)) continue;
       size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
       // Whole K whose unit slots do not fit: paired units (one slot per two steps of a block)
       // before K slices, e.g. the 248320-column vocabulary head at 1-4 rows (61 blocks x 10 steps

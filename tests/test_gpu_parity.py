@@ -465,11 +465,12 @@ def test_rowsplit_one_hot_is_exact_dequant(kind):
         assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
 
 
-# Small problems (every unit in a wave's ring from the start, all of x in LDS) take the row-split
-# kernel's SMALL form: 1-8 rows over N = 1024 (4 live rows per 16-row block), 5120 (20 rows per
-# workgroup) and 4112 (a partial last range), K = 5120 (x of 8 rows is 80 KB of LDS) and 2048.
-@pytest.mark.parametrize("m,k,n", [(1, 5120, 1024), (4, 5120, 5120), (5, 5120, 5120), (8, 5120, 5120),
-                                   (7, 2048, 4112), (2, 8192, 2048)])
+# Small problems: 6-8 rows over at most one row block per CU (every unit in a wave's ring from the
+# start, all of x in LDS) take the row-split kernel's SMALL form: N = 1024 (4 live rows per 16-row
+# block), 4096, 2048 at K = 8192 (x of 8 rows is 128 KB of LDS). 1-5 rows over small N take whole
+# K in the regular form (N = 1024; 5120 with 2 row blocks per CU; 4112, a partial last range).
+@pytest.mark.parametrize("m,k,n", [(6, 5120, 1024), (8, 5120, 1024), (7, 2048, 4096), (8, 8192, 2048),
+                                   (1, 5120, 1024), (4, 5120, 5120), (5, 5120, 5120), (3, 2048, 4112)])
 def test_rowsplit_small_shapes(m, k, n):
     note(f"row-split small {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, seed=m * 11 + k + n)
@@ -539,8 +540,8 @@ def test_rowsplit_own_blocks(m, k, n):
 
 
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
-@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (8, 34848), (16, 17408), (12, 34816), (2, 248320),
-                                 (6, 65984), (16, 248320), (7, 151936)])
+@pytest.mark.parametrize("m,n", [(8, 5120), (3, 1024), (6, 1024), (8, 34848), (16, 17408), (12, 34816),
+                                 (2, 248320), (6, 65984), (16, 248320), (7, 151936)])
 def test_rowsplit_small_and_eight_row_one_hot_is_exact_dequant(kind, m, n):
     """One-hot rows of x through the small form, the 8- and 16-row fragments, paired units and
     waves owning whole blocks: each output is one dequantized weight, equal to the oracle's bit for
