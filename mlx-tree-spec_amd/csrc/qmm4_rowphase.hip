@@ -566,7 +566,9 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   // ranges, half the K slices, the same walk) when those ranges would leave a workgroup at most
   // 3 phases, too few to pipeline: 32 / 64 x 5120 -> 5120 17.0 / 20.6 -> 16.0 / 19.4 us,
   // 16 / 32 x 17408 -> 5120 24.8 / 27.9 -> 22.6 / 26.5 us; with 6 phases (64 x 17408 -> 5120)
-  // the doubled x reads cost more (33.5 -> 37.2 us).
+  // the doubled x reads cost more (33.5 -> 37.2 us). They also replace them when their walk is
+  // strictly shorter: 48 / 64 x 5120 -> 10240 (80 ranges x 3 slices, 7 phases, against 40 x 6 of
+  // 4) 27.0 / 27.4 -> 24.3 / 26.2 us.
   auto narrow = [&](int c, int* phases) {
     int cm, cv, cb, items;
     size_t l;
@@ -593,7 +595,10 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
       }
     }
     const int id1 = pick(1);
-    if (id1 >= 0 && id1 != id && ph <= 3 && narrow(id1, &ph1) <= walk) id = id1;
+    if (id1 >= 0 && id1 != id) {
+      const long long walk1 = narrow(id1, &ph1);
+      if (walk1 < walk || (walk1 == walk && ph <= 3)) id = id1;
+    }
   }
   if (id < 0) return false;
   int cm, v, bpw, items;
