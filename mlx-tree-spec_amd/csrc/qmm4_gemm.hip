@@ -534,12 +534,19 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   plan->sk = false;
   plan->G = 0;
   plan->part_bytes = 0;
-  // Measured on MI355X (5120 -> 17408 and 17408 -> 5120 at 65 to 2048 rows): stream-K over
-  // 128 x 128 tiles wins while there are no more such tiles than CUs (1.9-3.2x at 65-256 rows);
-  // with more, whole 256 x 256 tiles (a 128 x 128 tile reads its LDS fragments for half as many
-  // MFMAs) are faster.
+  // Stream-K over 128 x 128 tiles while there are no more such tiles than CUs; beyond that, whole
+  // 256 x 256 tiles (a 128 x 128 tile reads its LDS fragments for half as many MFMAs) unless they
+  // would fill less than half the CUs (and there are at most 1.25 128-tiles per CU), or less than
+  // all of them with a half-empty last row of tiles (and at most 2 128-tiles per CU). Measured on
+  // MI355X (A/B, interleaved rounds): 192 / 256 / 384 x 5120 -> 17408 85.7 / 89.6 / 118.4 -> 71.5
+  // / 73.4 / 109.4 us (68 or 136 whole tiles), 1024 x 17408 -> 5120 278.3 -> 251.4 us (80 whole
+  // tiles); 1536 x 17408 -> 5120 (120 full whole tiles, 480 quarters) 316 us, 419 on stream-K;
+  // 512 and 1024 x 5120 -> 17408 (136 and 272 full tiles) stay on whole tiles.
   const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
-  if (tiles > c) return true;
+  const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
+  const bool sk = tiles <= c || (2 * tiles256 < c && 4 * tiles <= 5LL * c) ||
+                  (M % 256 != 0 && tiles256 < c && tiles <= 2LL * c);
+  if (!sk) return true;
   const bool sb8 = scale_rows_16b(s, b, K);
   const int ups = sb8 ? 8 : 2;
   const long long U = tiles * (K / BK / ups);

@@ -232,8 +232,11 @@ def workload_ref(x, w, s, b):
 # spread over every resident workgroup, tiles split between workgroups added by a fix-up kernel in
 # K order. 65 rows of the down projection (40 tiles over 17408 of K), the up projection at 128 rows,
 # K = 1152 (units of two K steps: K % 512 != 0), N = 784 and M = 200 (partial column and row tiles).
+# Also where whole 256 x 256 tiles would fill under half the CUs: 256 and 320 rows of the up
+# projection (272 and 408 tiles of 128), 1024 rows of the down projection (320 tiles).
 @pytest.mark.parametrize("m,k,n", [(65, 17408, 5120), (128, 5120, 17408), (100, 1152, 4096), (200, 5120, 784),
-                                   (96, 512, 1024)])
+                                   (96, 512, 1024), (256, 5120, 17408), (320, 5120, 17408),
+                                   (1024, 17408, 5120)])
 def test_gemm_stream_k_shapes(m, k, n):
     note(f"stream-K {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=m * 19 + k + n)
