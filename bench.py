@@ -68,7 +68,7 @@ SHARD8 = {
 }
 # The dominant kernel of the headline workload and the committed rocprofv3 summaries the roofline
 # record reads (the traffic figure is used only if its summary names this kernel).
-HEAD_KERNEL = "rowsplit_kernel<4, 4, false, false, false, false, false>"
+HEAD_KERNEL = "rowsplit_kernel<4, 4, false, false, false, false, 0, false>"
 TRACE_PROFILE = "qmm4_bench_workloads_kernel_trace.txt"
 TRAFFIC_PROFILE = "rowsplit_decode_gate_up_traffic.txt"
 DESCR = {

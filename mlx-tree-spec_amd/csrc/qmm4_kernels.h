@@ -81,7 +81,8 @@ struct RowSplitPlan {
   int MP;       // x rows per A fragment (4 or 8)
   bool small;   // every unit in flight from the start, all of x in LDS, sums in registers
   bool xreg;    // 9-16 rows over a small problem: x loaded straight into registers per K chunk
-  bool pair;    // whole K with units taken in pairs (consecutive steps of a block, one slot per pair)
+  bool pair;    // whole K with units taken in groups (consecutive steps of a block, one slot per group)
+  int GU;       // units per group when pair
   bool own;     // whole K, each wave owning whole blocks with their sums in registers (no slots)
   int V;        // super-steps (128 k) per unit
   bool fused;   // fused gate+up: y = silu(x w_gate^T) * (x w_up^T), w = [w_gate; w_up]

@@ -33,10 +33,10 @@
 //  * Small problems (every unit fits the waves' rings at once, all of x fits LDS): the SMALL form
 //    fetches every unit at the start, loads x straight into LDS behind those fetches, and keeps
 //    each wave's two unit sums in registers until x is dead; the slots then take the x area.
-//  * Whole K over a large N whose slots do not fit (vocabulary heads): PAIR takes units two at a
-//    time (consecutive steps of one block, one slot per pair); OWN (5-16 rows, x alone filling up
-//    to all of LDS) gives wave w blocks w, w + 16, ... whole, their sums kept in registers and
-//    stored to y as each block's last step is done.
+//  * Whole K over a large N whose slots do not fit (vocabulary heads): PAIR takes units in groups
+//    of consecutive steps of one block, one slot per group (pairs at 1-4 rows, groups of 5 at 5-8);
+//    OWN (9-16 rows, x alone filling up to all of LDS) gives wave w blocks w, w + 16, ... whole,
+//    their sums kept in registers and stored to y as each block's last step is done.
 //  * Fused gate+up (FUSED): w is [w_gate; w_up] (N rows, up rows from N / 2), y is [M, N / 2] =
 //    silu(x @ w_gate^T) * (x @ w_up^T). Workgroup p owns output columns [p R, p R + R); its 2R
 //    weight rows are listed gate rows first, then the up rows of the same columns (N / 2 further),
@@ -82,6 +82,7 @@ struct RowSplitParams {
   int SU;    // units per block, Kp / (128 V)
   int KS;    // K slices per column range (1: each workgroup all of K)
   int Kp;    // K per slice
+  int GU;    // PAIR: units per slot group (a divisor of SU, at least 2)
   float* part;    // KS > 1: fp32 row sums [workgroup][row] (f32x4 over the rows of x)
   uint32_t* cnt;  // KS > 1: arrivals per column range (0 between launches)
   // NORM: x is the residual stream's x, normalised while staged (see the kernel), with
@@ -138,7 +139,8 @@ __host__ __device__ inline size_t rowsplit_red_offset(int Kp, int MP, int units,
 // then the 4 waves in order), so the staged rows are the bits that kernel would store for n, and y
 // is the bits of the unfused pair. Each workgroup reads all of x and r (from L2 after the first),
 // stages its K slice of n, and workgroup 0 writes h and n.
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false, bool OWN = false>
+// PAIR: 0, or units taken in groups: 1 for pairs, 2 for groups of P.GU > 2.
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, int PAIR = 0, bool OWN = false>
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "x rows per fragment");
@@ -152,9 +154,9 @@ void rowsplit_kernel(RowSplitParams P) {
   const int S = P.Kp >> 7;  // super-steps per row in this workgroup's K slice
   const int SU = P.SU;
   const int U = P.RB * SU;
-  // PAIR: a wave takes units 2p and 2p + 1 (consecutive steps of one block; SU is even) together
-  // and leaves their sum in one slot, so a block has SU / 2 slots.
-  const int SS = PAIR ? SU / 2 : SU;
+  // PAIR: a wave takes units in groups of GU consecutive steps of one block (GU divides SU) and
+  // leaves each group's sum in one slot, so a block has SU / GU slots.
+  const int SS = PAIR ? SU / P.GU : SU;
   u32x4* xs = reinterpret_cast<u32x4*>(lds);
   // SMALL: the slots take over the x area once x is dead.
   f32x4* part = reinterpret_cast<f32x4*>(lds + (SMALL ? 0 : rowsplit_xs_bytes(P.Kp, MP)));
@@ -294,12 +296,12 @@ void rowsplit_kernel(RowSplitParams P) {
   // OWN: wave w takes the SU steps of blocks w, w + 16, ... in turn; q counts its units.
   const int own_nq = OWN && wave < P.RB ? (P.RB - wave + kRsWaves - 1) / kRsWaves * SU : 0;
   auto own_unit = [&](int q) { return q < own_nq ? (wave + kRsWaves * (q / SU)) * SU + q % SU : U; };
-  int ua = PAIR ? 2 * wave : wave, ub = PAIR ? 2 * wave + 1 : wave + kRsWaves;
+  int ua = PAIR ? P.GU * wave : wave, ub = PAIR ? P.GU * wave + 1 : wave + kRsWaves;
   if constexpr (OWN) {
     ua = own_unit(0);
     ub = own_unit(1);
   }
-  // Units (pairs) handed out by the LDS counter after the ring's first fill.
+  // Units (groups) handed out by the LDS counter after the ring's first fill.
   constexpr int kFirst = PAIR ? kRsWaves : kRsPF * kRsWaves;
   if constexpr (!KSPLIT) {
     fetch(0, ua);
@@ -483,9 +485,12 @@ void rowsplit_kernel(RowSplitParams P) {
     if (q < own_nq) step(q, ua, std::integral_constant<int, 0>{});
     return;
   } else if constexpr (PAIR) {
-    // Half 0 of the pair from slot 0, slot 0 refilled with the next pair's half 0, half 1 from
-    // slot 1 added to the same sums, slot 1 refilled with the next pair's half 1.
-    auto half = [&](int u, auto jc, f32x4 acc) __attribute__((always_inline)) {
+    // The wave's units in sequence alternate between the ring's slots; the unit after a group's
+    // last is the first of the next group taken from the counter. After computing a slot's unit
+    // into the group's sums, the slot is refilled with the unit two ahead; a group's sums go to
+    // its slot after its last unit.
+    const int GU = P.GU;
+    auto one = [&](int u, auto jc, f32x4 acc) __attribute__((always_inline)) {
       constexpr int j = decltype(jc)::value;
       const int st = u - (u / SU) * SU;
       bool bad = false;
@@ -497,21 +502,54 @@ void rowsplit_kernel(RowSplitParams P) {
       if (__builtin_amdgcn_ballot_w64(bad) == 0) return compute(j, st, std::true_type{}, acc);
       return compute(j, st, std::false_type{}, acc);
     };
-    while (ua < U) {
+    // (A group taken one group ahead, to hide the atomic's round trip, made pairs 9% slower.)
+    auto succ = [&](int u) __attribute__((always_inline)) {
+      if ((u + 1) % GU != 0) return u + 1;
       int taken = 0;
       if (lane == 0) taken = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-      const int np = __builtin_amdgcn_readfirstlane(taken);
-      f32x4 acc = half(ua, std::integral_constant<int, 0>{}, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
-      fetch(0, 2 * np);
-      acc = half(ub, std::integral_constant<int, 1>{}, acc);
-      if (g < G) part[((ua >> 1) * G + g) * 16 + n] = acc;
-      ++ndone;
-      if (ndone == 1) __builtin_amdgcn_s_setprio(2);
-      else if (ndone == 2) __builtin_amdgcn_s_setprio(1);
-      else if (ndone == 3) __builtin_amdgcn_s_setprio(0);
-      fetch(1, 2 * np + 1);
-      ua = 2 * np;
-      ub = ua + 1;
+      return __builtin_amdgcn_readfirstlane(taken) * GU;
+    };
+    f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+    // Slot J's unit u is computed, then u becomes the unit after `other` (the next in sequence).
+    auto step = [&](int& u, int other, auto jc) __attribute__((always_inline)) {
+      constexpr int j = decltype(jc)::value;
+      acc = one(u, jc, acc);
+      if ((u + 1) % GU == 0) {
+        if (g < G) part[((u / GU) * G + g) * 16 + n] = acc;
+        acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+        ++ndone;
+        if (ndone == 1) __builtin_amdgcn_s_setprio(2);
+        else if (ndone == 2) __builtin_amdgcn_s_setprio(1);
+        else if (ndone == 3) __builtin_amdgcn_s_setprio(0);
+      }
+      u = succ(other);
+      fetch(j, u);
+    };
+    if constexpr (PAIR == 1) {
+      // Pairs: the next pair is taken before this one's MFMAs, its half 0 fetched into slot 0 as
+      // soon as this pair's half 0 is done (measured 3% faster than the general walk below).
+      while (ua < U) {
+        int taken = 0;
+        if (lane == 0) taken = __hip_atomic_fetch_add(next, 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        const int np = __builtin_amdgcn_readfirstlane(taken);
+        acc = one(ua, std::integral_constant<int, 0>{}, f32x4{0.0f, 0.0f, 0.0f, 0.0f});
+        fetch(0, 2 * np);
+        acc = one(ub, std::integral_constant<int, 1>{}, acc);
+        if (g < G) part[((ua >> 1) * G + g) * 16 + n] = acc;
+        ++ndone;
+        if (ndone == 1) __builtin_amdgcn_s_setprio(2);
+        else if (ndone == 2) __builtin_amdgcn_s_setprio(1);
+        else if (ndone == 3) __builtin_amdgcn_s_setprio(0);
+        fetch(1, 2 * np + 1);
+        ua = 2 * np;
+        ub = ua + 1;
+      }
+    } else {
+      while (ua < U) {
+        step(ua, ub, std::integral_constant<int, 0>{});
+        if (ub >= U) break;
+        step(ub, ua, std::integral_constant<int, 1>{});
+      }
     }
   } else {
     for (;;) {
@@ -760,6 +798,7 @@ bool rowsplit_xreg_plan(int M, int N, int K, int cus, RowSplitPlan* plan) {
   plan->small = true;
   plan->xreg = true;
   plan->pair = false;
+  plan->GU = 0;
   plan->own = false;
   plan->V = kXrV;
   plan->fused = false;
@@ -810,6 +849,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       plan->small = true;
       plan->xreg = false;
       plan->pair = false;
+      plan->GU = 0;
       plan->own = false;
       plan->V = 4;
       plan->fused = false;
@@ -853,15 +893,20 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       const int SU = S / V;
       if (MP == 4 && pass == 0 && (ks == 1 ? RB < 4 && K > 8192 : RB * SU < 3 * kRsWaves)) continue;
       size_t smem = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU, MP) + 32;
-      // Whole K whose unit slots do not fit: paired units (one slot per two steps of a block)
-      // before K slices, e.g. the 248320-column vocabulary head at 1-4 rows (61 blocks x 10 steps
-      // per CU) or the 65984-column head at 5-8 rows.
+      // Whole K whose unit slots do not fit: units in groups of the fewest steps that fit (one slot
+      // per group) before K slices, e.g. pairs over the 248320-column vocabulary head at 1-4 rows
+      // (61 blocks x 10 steps per CU) or the 65984-column head at 5-8 rows, groups of 5 over the
+      // 248320- and 151936-column heads at 5-8 rows (163.7-172.3 -> 145.9-147.9 us and 108.1 ->
+      // 97.8 us against waves owning whole blocks).
       bool pair = false;
-      if (smem > 160 * 1024 && ks == 1 && !fused && V == 4 && SU % 2 == 0) {
-        const size_t ps = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU / 2, MP) + 32;
+      int gu = 0;
+      for (int c = 2; c <= SU && smem > 160 * 1024 && ks == 1 && !fused && V == 4; ++c) {
+        if (SU % c != 0) continue;
+        const size_t ps = rowsplit_xs_bytes(kp, MP) + rowsplit_part_bytes(RB * SU / c, MP) + 32;
         if (ps <= 160 * 1024) {
           smem = ps;
           pair = true;
+          gu = c;
         }
       }
       // Neither fits, but all of x does and a CU has at least two blocks per wave: each wave takes
@@ -879,6 +924,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
       plan->small = false;
       plan->xreg = false;
       plan->pair = pair;
+      plan->GU = gu;
       plan->own = own;
       plan->V = V;
       plan->fused = fused;
@@ -905,7 +951,7 @@ size_t rowsplit_smem(const RowSplitPlan& plan, bool norm) {
                                  sizeof(float) * (kRsThreads / 64));
 }
 
-template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, bool PAIR = false, bool OWN = false>
+template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, int PAIR = 0, bool OWN = false>
 hipError_t launch_rowsplit_t(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   static bool attr_set = false;
   if (!attr_set) {
@@ -930,8 +976,10 @@ template <int MP, bool NORM>
 hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
   if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true, NORM>(plan, P, stream);
   if constexpr (!NORM) {
-    if (plan.pair) return launch_rowsplit_t<MP, 4, false, false, false, false, true>(plan, P, stream);
-    if (plan.own) return launch_rowsplit_t<MP, 4, false, false, false, false, false, true>(plan, P, stream);
+    if (plan.pair)
+      return plan.GU == 2 ? launch_rowsplit_t<MP, 4, false, false, false, false, 1>(plan, P, stream)
+                          : launch_rowsplit_t<MP, 4, false, false, false, false, 2>(plan, P, stream);
+    if (plan.own) return launch_rowsplit_t<MP, 4, false, false, false, false, 0, true>(plan, P, stream);
   }
   if (plan.fused)
     return plan.V == 5 ? launch_rowsplit_k<MP, 5, true, NORM>(plan, P, stream)
@@ -960,6 +1008,7 @@ hipError_t launch_rowsplit(const RowSplitPlan& plan, const uint16_t* x, const ui
   P.M = M; P.N = N; P.K = K;
   P.Nout = plan.Nout; P.R = plan.R; P.RB = plan.RB; P.SU = plan.SU;
   P.KS = plan.KS; P.Kp = plan.Kp; P.part = part; P.cnt = cnt;
+  P.GU = plan.pair ? plan.GU : 1;
   P.r = norm ? norm->r : nullptr;
   P.nw = norm ? norm->weight : nullptr;
   P.h_out = norm ? norm->h : nullptr;

@@ -512,11 +512,13 @@ def test_rowsplit_sixteen_row_shapes(m, k, n):
         assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
-# Whole K with units taken in pairs (two consecutive steps of a block summed into one LDS slot)
-# where one slot per step does not fit: 1-4 rows over the 248320-column vocabulary head (61 blocks
-# x 10 steps per CU; N = 248336 leaves a partial last range), 6 rows over the 65984-column head
-# (8-row fragments), 2 rows at K = 4096 (8 steps per block).
-@pytest.mark.parametrize("m,k,n", [(3, 5120, 248336), (6, 5120, 65984), (2, 4096, 262144)])
+# Whole K with units taken in groups (consecutive steps of a block summed into one LDS slot) where
+# one slot per step does not fit: pairs for 1-4 rows over the 248320-column vocabulary head (61
+# blocks x 10 steps per CU; N = 248336 leaves a partial last range), 6 rows over the 65984-column
+# head (8-row fragments), 2 rows at K = 4096 (8 steps per block); groups of 5 for 5-8 rows over
+# the 248320- and 151936-column heads (x of 8 rows leaves room for 2 slots per block).
+@pytest.mark.parametrize("m,k,n", [(3, 5120, 248336), (6, 5120, 65984), (2, 4096, 262144), (5, 5120, 248320),
+                                   (8, 5120, 151936)])
 def test_rowsplit_paired_units(m, k, n):
     note(f"row-split paired units {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, seed=m * 29 + k + n)
@@ -527,11 +529,11 @@ def test_rowsplit_paired_units(m, k, n):
         assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
-# Whole K where neither one slot per step nor per pair fits but all of x does, with at least two
-# blocks per wave: each wave owns whole blocks and keeps their sums in registers. 5-16 rows over
-# the 248320-column vocabulary head (61 blocks per CU; 16 rows fill all 160 KB of LDS with x),
-# N = 248336 (a partial last range), 12 rows over the 151936-column head, K = 4096.
-@pytest.mark.parametrize("m,k,n", [(16, 5120, 248336), (5, 5120, 248320), (12, 5120, 151936), (9, 4096, 262144)])
+# Whole K where no grouping of slots fits but all of x does, with at least two blocks per wave:
+# each wave owns whole blocks and keeps their sums in registers. 9-16 rows over the 248320-column
+# vocabulary head (61 blocks per CU; 16 rows fill all 160 KB of LDS with x), N = 248336 (a partial
+# last range), 12 rows over the 151936-column head, 131072 columns (32 blocks per CU), K = 4096.
+@pytest.mark.parametrize("m,k,n", [(16, 5120, 248336), (12, 5120, 151936), (16, 5120, 131072), (9, 4096, 262144)])
 def test_rowsplit_own_blocks(m, k, n):
     note(f"row-split own blocks {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, seed=m * 37 + k + n)
