@@ -682,41 +682,44 @@ void rowsplit_xreg_kernel(RowSplitParams P) {
   u32x4 xa[NCH][V][4];
   u32x4 wv[NCH][kXrMaxRB][V];
   Scales<V> sv[NCH][kXrMaxRB], bv[NCH][kXrMaxRB];
-  // Issue every load of this wave's chunks: weights first (from HBM), then x (from L2).
+  // Issue every load of this wave's chunks in two halves of its super-steps, each half's weights
+  // (from HBM) before its x (from L2): the first half's MFMAs need only the first half's loads
+  // (16 x 5120 -> 5120 14.5 -> 14.3 us, 9 rows 13.1 -> 12.9 us; quarters were no better).
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int st = wave + c * kXrMaxWaves;
-    const bool live = st < SU;
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(P.w), 0,
-                                                                        live ? wrec : 0, kBufferRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.s), 0,
-                                                                        live ? srec : 0, kBufferRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.b), 0,
-                                                                        live ? srec : 0, kBufferRsrcWord3);
+  for (int h = 0; h < 2; ++h) {
 #pragma unroll
-    for (int b = 0; b < kXrMaxRB; ++b) {
-      const int row = r0 + b * 16 + n;
-      const bool ok = b < RB && row < r1;
-      const uint32_t wo = ok ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
-      const uint32_t so = ok ? (uint32_t)row * (uint32_t)KG * 2u : kOut;
+    for (int c = 0; c < NCH; ++c) {
+      const int st = wave + c * kXrMaxWaves;
+      const bool live = st < SU;
+      const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint32_t*>(P.w), 0,
+                                                                          live ? wrec : 0, kBufferRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.s), 0,
+                                                                          live ? srec : 0, kBufferRsrcWord3);
+      const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(P.b), 0,
+                                                                          live ? srec : 0, kBufferRsrcWord3);
 #pragma unroll
-      for (int v = 0; v < V; ++v)
-        wv[c][b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + v * 64, live ? st * V * 64 : 0, 0);
-      sv[c][b] = load_scales<V>(rs, so, live ? st * 4 * V : 0);
-      bv[c][b] = load_scales<V>(rb, so, live ? st * 4 * V : 0);
-    }
-  }
+      for (int b = 0; b < kXrMaxRB; ++b) {
+        const int row = r0 + b * 16 + n;
+        const bool ok = b < RB && row < r1;
+        const uint32_t wo = ok ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
+        const uint32_t so = ok ? (uint32_t)row * (uint32_t)KG * 2u : kOut;
+        if (h == 0) {
+          sv[c][b] = load_scales<V>(rs, so, live ? st * 4 * V : 0);
+          bv[c][b] = load_scales<V>(rb, so, live ? st * 4 * V : 0);
+        }
 #pragma unroll
-  for (int c = 0; c < NCH; ++c) {
-    const int st = wave + c * kXrMaxWaves;
-    const bool live = st < SU;
-#pragma unroll
-    for (int v = 0; v < V; ++v)
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt) {
-        const uint32_t off = live ? xrow + (uint32_t)(st * V * 128 + v * 128 + g * 32 + tt * 8) * 2u : 0x80000000u;
-        xa[c][v][tt] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+        for (int v = h * V / 2; v < (h + 1) * V / 2; ++v)
+          wv[c][b][v] = __builtin_amdgcn_raw_buffer_load_b128(rw, wo + v * 64, live ? st * V * 64 : 0, 0);
       }
+#pragma unroll
+      for (int v = h * V / 2; v < (h + 1) * V / 2; ++v)
+#pragma unroll
+        for (int tt = 0; tt < 4; ++tt) {
+          const uint32_t off = live ? xrow + (uint32_t)(st * V * 128 + v * 128 + g * 32 + tt * 8) * 2u : 0x80000000u;
+          xa[c][v][tt] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
   }
 
 #pragma unroll
