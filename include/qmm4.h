@@ -51,8 +51,8 @@ extern "C" {
  *   (M + 256) * N * 2 bytes below 2^32), x and w 16-byte aligned, scales and biases
  *   4-byte aligned, y 2-byte aligned. M == 0 or N == 0 is a no-op. Rows M <= 64 run one of the
  *   HBM-bound verify/decode kernels (row-split's x-in-registers form for 9-16 rows over small
- *   problems; row-split for M <= 16 when its plan fits: whole K (units taken in pairs, or waves
- *   owning whole blocks, when N is as large as a vocabulary head) or a few K slices per workgroup,
+ *   problems; row-split for M <= 16 when its plan fits: whole K (units taken in groups of
+ *   consecutive steps, or waves owning whole blocks, when N is as large as a vocabulary head) or a few K slices per workgroup,
  *   every unit in flight at once for small problems; row-phase for more than 16 rows, a large N,
  *   or fewer rows when its K split fills half the CUs; K-split verify or stream-K skinny
  *   otherwise), larger M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles
