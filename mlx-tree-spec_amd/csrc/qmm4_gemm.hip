@@ -554,7 +554,7 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   if (G > U) G = U;
   const size_t slot = (size_t)GemmCfg<128, 128>::kPartF4 * 16 * 2;  // two partial tiles per workgroup
   if ((size_t)G * slot > ws_capacity) G = (long long)(ws_capacity / slot);
-  if (G < c / 2) return true;  // too little workspace to spread the tiles: whole tiles instead
+  if (G < 1 || G < c / 2) return true;  // too little workspace to spread the tiles: whole tiles instead
   plan->sk = true;
   plan->G = (int)G;
   plan->part_bytes = (size_t)G * slot;
