@@ -119,6 +119,26 @@ void check_rowphase(int M, int N, int K, int cus) {
 #undef RP
 }
 
+void check_verify(int M, int N, int K, int cus) {
+  for (int vmax : {1, 2, 4})
+    for (int occ : {1, 2}) {
+      VerifyPlan p{};
+      if (!verify_plan(M, N, K, vmax, cus, occ, &p)) continue;
+      ++g_checked;
+      const char* f = "verify M=%d N=%d K=%d cus=%d vmax=%d occ=%d";
+#define VP(cond) CHECK(cond, f, M, N, K, cus, vmax, occ)
+      VP(p.variant >= 0 && p.variant < kVerifyVariants);
+      VP(p.steps_v >= 1 && p.steps_v <= vmax && K % (128 * p.steps_v) == 0);
+      VP(p.tile_cols >= 1 && (long long)p.tiles * p.tile_cols >= N &&
+         (long long)(p.tiles - 1) * p.tile_cols < N);
+      VP(p.units == (long long)p.tiles * (K / (128 * p.steps_v)));
+      VP(p.blocks >= 1 && p.blocks <= p.units);
+      VP(p.threads >= 64 && p.threads <= 1024 && p.threads % 64 == 0);
+      VP(p.lds <= kLds);
+#undef VP
+    }
+}
+
 void check_gemm(int M, int N, int K, int cus) {
   const uint16_t* s = reinterpret_cast<const uint16_t*>(uintptr_t{0x100000});
   const uint16_t* b = reinterpret_cast<const uint16_t*>(uintptr_t{0x200000});
@@ -159,6 +179,7 @@ int main() {
             check_xreg(M, N, K, cus);
           }
           if (M <= 64) check_rowphase(M, N, K, cus);
+          if (M <= 64) check_verify(M, N, K, cus);
           else check_gemm(M, N, K, cus);
         }
   std::printf("plans checked: %lld, violations: %lld\n", g_checked, g_fail);

@@ -1,7 +1,7 @@
 """Kernel planners against what their kernels assume (CPU only, no GPU call).
 
 tests/plan_invariants.cpp calls the planners exported by the built libqmm4.so (row-split, its
-x-in-registers form, row-phase, GEMM) over a grid of shapes (1-4096 rows, 16-262144 columns,
+x-in-registers form, row-phase, K-split verify, GEMM) over a grid of shapes (1-4096 rows, 16-262144 columns,
 K = 128-20480) and CU counts (1-304), and checks every accepted plan: dynamic LDS within 160 KB,
 output columns covered exactly once, K slices and units that tile K, each loop form only in the
 configuration its launch path instantiates, stream-K workgroups between 1 and the unit count
