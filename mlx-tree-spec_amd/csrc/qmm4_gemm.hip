@@ -31,6 +31,8 @@
 //    with a 2-step ring); a workgroup's first and last segments may cover part of a tile and leave fp32 partial
 //    tiles, which gemm_sk_reduce_kernel adds in K order (the same bits whichever workgroup ran a
 //    segment).
+//  * Long K (>= 8192) with fewer whole 256 x 256 tiles than CUs and at least 256 rows (512-2048
+//    rows of the down projection): the same stream-K over 256 x 256 tiles, one workgroup per CU.
 // The output tile is staged through LDS and stored as 16-byte row chunks.
 #include <type_traits>
 
@@ -528,12 +530,35 @@ bool scale_rows_16b(const uint16_t* s, const uint16_t* b, int K) {
 // launch; when the last round would leave most CUs idle, its tiles are cut into 128 x 128 quarters
 // and launched next. Fewer tiles (e.g. a short prompt tail or more than 64 tree nodes over a
 // narrow output): stream-K over 128 x 128 tiles, the tiles x K units split evenly over every
-// resident workgroup slot, then the fix-up of the split tiles.
+// resident workgroup slot, then the fix-up of the split tiles; with long K and fewer whole
+// 256 x 256 tiles than CUs, stream-K over those instead.
 bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t* s, const uint16_t* b, GemmPlan* plan) {
   const int c = cus > 0 ? cus : 1;
   plan->sk = false;
+  plan->sk256 = false;
   plan->G = 0;
   plan->part_bytes = 0;
+  const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
+  // Stream-K over 256 x 256 tiles (one workgroup per CU, 8-step units): at least 256 rows, K of
+  // 8192 or more, fewer whole tiles than CUs and at least 3.5 units per workgroup. A 256-tile step
+  // does 4x the MFMAs of a 128-tile step in ~2.1x the time, against 4x the partial-tile bytes
+  // (~128 MB written and read back at 256 CUs, ~40 us), so it pays where K gives each workgroup
+  // enough steps. Measured (A/B, interleaved rounds, against the rules below): 512 / 768 / 1024 /
+  // 1536 x 17408 -> 5120 150.6 / 216.2 / 246.6 / 327.1 -> 120.5 / 151.7 / 195.0 / 271.9 us,
+  // 512 x 12288 -> 5120 107.5 -> 91.0 us, 1024 x 8192 -> 5120 122.4 -> 108.5 us, 512 x 17408 ->
+  // 10240 244.5 -> 196.3 us; slower with fewer units per workgroup (256 x 8192 -> 5120 44.0 -> 59.6
+  // us, 256 x 12288 -> 6144 64.0 -> 68.7 us) and at K = 5120 (the up projection at 256-4096 rows,
+  // 2-13% slower).
+  if (M >= 256 && K >= 8192 && tiles256 < c && scale_rows_16b(s, b, K) && 2 * tiles256 * (K / 512) >= 7LL * c) {
+    const size_t slot256 = (size_t)GemmCfg<256, 256>::kPartF4 * 16 * 2;
+    if ((size_t)c * slot256 <= ws_capacity) {
+      plan->sk = true;
+      plan->sk256 = true;
+      plan->G = c;
+      plan->part_bytes = (size_t)c * slot256;
+      return true;
+    }
+  }
   // Stream-K over 128 x 128 tiles while there are no more such tiles than CUs; beyond that, whole
   // 256 x 256 tiles (a 128 x 128 tile reads its LDS fragments for half as many MFMAs) unless they
   // would fill less than half the CUs (and there are at most 1.25 128-tiles per CU), or less than
@@ -543,7 +568,6 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   // tiles); 1536 x 17408 -> 5120 (120 full whole tiles, 480 quarters) 316 us, 419 on stream-K;
   // 512 and 1024 x 5120 -> 17408 (136 and 272 full tiles) stay on whole tiles.
   const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
-  const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
   const bool sk = tiles <= c || (2 * tiles256 < c && 4 * tiles <= 5LL * c) ||
                   (M % 256 != 0 && tiles256 < c && tiles <= 2LL * c);
   if (!sk) return true;
@@ -569,6 +593,20 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
   P.sk = 0; P.upt = 0; P.ups = 0; P.U = 0; P.part = part;
   // 16-byte loads of 8 groups need 16-byte aligned scale rows and pointers.
   const bool sb8 = scale_rows_16b(s, b, K);
+  if (plan.sk256) {
+    if (!sb8) return hipErrorInvalidValue;
+    P.tiles_m = (M + 255) / 256;
+    P.tiles_n = (N + 255) / 256;
+    P.tile0 = 0;
+    P.quarter = 0;
+    P.sk = 1;
+    P.ups = 8;
+    P.upt = K / BK / P.ups;
+    P.U = (long long)P.tiles_m * P.tiles_n * P.upt;
+    hipError_t e = launch_tiles<256, 256, true>(P, plan.G, stream);
+    if (e != hipSuccess) return e;
+    return launch_sk_reduce<256, 256>(P, plan.G, stream);
+  }
   if (plan.sk) {
     P.tiles_m = (M + 127) / 128;
     P.tiles_n = (N + 127) / 128;

@@ -134,10 +134,11 @@ hipError_t launch_add_rms_norm(const uint16_t* x, const uint16_t* r, const uint1
 hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 
 // LDS-tiled MFMA GEMM for M > 64: whole 256 x 256 tiles when there are more 128 x 128 tiles than
-// CUs, otherwise stream-K over 128 x 128 tiles (fp32 partials of split tiles in the workspace,
-// added by a fix-up kernel behind the first).
+// CUs, otherwise stream-K over 128 x 128 tiles, or over 256 x 256 tiles for long K and few tiles
+// (fp32 partials of split tiles in the workspace, added by a fix-up kernel behind the first).
 struct GemmPlan {
   bool sk;            // stream-K
+  bool sk256;         // stream-K over 256 x 256 tiles (else 128 x 128)
   int G;              // stream-K workgroups
   size_t part_bytes;  // stream-K partial tiles (two per workgroup)
 };

@@ -149,13 +149,15 @@ void check_gemm(int M, int N, int K, int cus) {
     const char* f = "gemm M=%d N=%d K=%d cus=%d cap=%zu";
 #define GP(cond) CHECK(cond, f, M, N, K, cus, cap)
     if (p.sk) {
-      const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
+      const int t = p.sk256 ? 256 : 128;
+      const long long tiles = (long long)((M + t - 1) / t) * ((N + t - 1) / t);
       const long long units = tiles * (K / 64 / (K % 512 == 0 ? 8 : 2));
       GP(p.G >= 1 && p.G <= units);
-      GP(p.part_bytes == (size_t)p.G * 128 * 128 * 4 * 2);
+      GP(p.part_bytes == (size_t)p.G * t * t * 4 * 2);
       GP(p.part_bytes <= cap);
+      if (p.sk256) GP(K % 512 == 0 && M >= 256 && p.G == cus);  // 8-step units, one workgroup per CU
     } else {
-      GP(p.part_bytes == 0);
+      GP(!p.sk256 && p.part_bytes == 0);
     }
 #undef GP
   }
