@@ -56,8 +56,9 @@ extern "C" {
  *   every unit in flight at once for small problems; row-phase for more than 16 rows, a large N,
  *   or fewer rows when its K split fills half the CUs; K-split verify or stream-K skinny
  *   otherwise), larger M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles
- *   when whole tiles would leave many CUs idle); the choice is a fixed function of the shape and the
- *   scale/bias alignment. Results are deterministic (bit-identical across calls and streams).
+ *   when whole tiles would leave many CUs idle, over 256 x 256 tiles when K is long as well);
+ *   the choice is a fixed function of the shape and the scale/bias alignment. Results are
+ *   deterministic (bit-identical across calls and streams).
  */
 int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
                      void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
