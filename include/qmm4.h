@@ -56,7 +56,7 @@ extern "C" {
  *   every unit in flight at once for small problems; row-phase for more than 16 rows, a large N,
  *   or fewer rows when its K split fills half the CUs; K-split verify or stream-K skinny
  *   otherwise), larger M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles
- *   when whole tiles would leave many CUs idle, over 256 x 256 tiles when K is long as well);
+ *   when whole tiles would leave many CUs idle, over 256 x 256 tiles when K is long too);
  *   the choice is a fixed function of the shape and the scale/bias alignment. Results are
  *   deterministic (bit-identical across calls and streams).
  */

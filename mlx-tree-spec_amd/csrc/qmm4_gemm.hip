@@ -31,8 +31,8 @@
 //    with a 2-step ring); a workgroup's first and last segments may cover part of a tile and leave fp32 partial
 //    tiles, which gemm_sk_reduce_kernel adds in K order (the same bits whichever workgroup ran a
 //    segment).
-//  * Long K (>= 8192) with fewer whole 256 x 256 tiles than CUs and at least 256 rows (512-2048
-//    rows of the down projection): the same stream-K over 256 x 256 tiles, one workgroup per CU.
+//  * Long K (>= 8192) with whole 256 x 256 tiles for at most 70% of the CUs and at least 256 rows
+//    (512-2048 rows of the down projection): the same stream-K over 256 x 256 tiles, one workgroup per CU.
 // The output tile is staged through LDS and stored as 16-byte row chunks.
 #include <type_traits>
 
@@ -540,16 +540,18 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   plan->part_bytes = 0;
   const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
   // Stream-K over 256 x 256 tiles (one workgroup per CU, 8-step units): at least 256 rows, K of
-  // 8192 or more, fewer whole tiles than CUs and at least 3.5 units per workgroup. A 256-tile step
+  // 8192 or more, whole tiles for at most 70% of the CUs and at least 3.5 units per workgroup. A 256-tile step
   // does 4x the MFMAs of a 128-tile step in ~2.1x the time, against 4x the partial-tile bytes
   // (~128 MB written and read back at 256 CUs, ~40 us), so it pays where K gives each workgroup
   // enough steps. Measured (A/B, interleaved rounds, against the rules below): 512 / 768 / 1024 /
   // 1536 x 17408 -> 5120 150.6 / 216.2 / 246.6 / 327.1 -> 120.5 / 151.7 / 195.0 / 271.9 us,
   // 512 x 12288 -> 5120 107.5 -> 91.0 us, 1024 x 8192 -> 5120 122.4 -> 108.5 us, 512 x 17408 ->
   // 10240 244.5 -> 196.3 us; slower with fewer units per workgroup (256 x 8192 -> 5120 44.0 -> 59.6
-  // us, 256 x 12288 -> 6144 64.0 -> 68.7 us) and at K = 5120 (the up projection at 256-4096 rows,
-  // 2-13% slower).
-  if (M >= 256 && K >= 8192 && tiles256 < c && scale_rows_16b(s, b, K) && 2 * tiles256 * (K / 512) >= 7LL * c) {
+  // us, 256 x 12288 -> 6144 64.0 -> 68.7 us), at K = 5120 (the up projection at 256-4096 rows,
+  // 2-13% slower) and with whole tiles for most CUs (2560 / 3072 x 17408 -> 5120, 200 / 240 tiles:
+  // 413.9 / 446.0 -> 417.3 / 490.2 us; 2048 rows, 160 tiles: 358.9 -> 340.8 us).
+  if (M >= 256 && K >= 8192 && 10 * tiles256 <= 7LL * c && scale_rows_16b(s, b, K) &&
+      2 * tiles256 * (K / 512) >= 7LL * c) {
     const size_t slot256 = (size_t)GemmCfg<256, 256>::kPartF4 * 16 * 2;
     if ((size_t)c * slot256 <= ws_capacity) {
       plan->sk = true;
