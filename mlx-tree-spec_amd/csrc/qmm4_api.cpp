@@ -347,7 +347,7 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
     gemm_plan((int)M, (int)N, (int)K, di->cus, ws.capacity(), sb, bb, &gplan);
     uint32_t* gcnt = nullptr;
     float* gpart = nullptr;
-    if (gplan.sk) {
+    if (gplan.part_bytes > 0) {
       rc = ws.get(0, gplan.part_bytes, &gcnt, &gpart);
       if (rc) return rc;
     }

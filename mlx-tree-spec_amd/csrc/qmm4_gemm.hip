@@ -67,6 +67,8 @@ struct GemmParams {
   // a tile and then leave fp32 partial tiles in part[(workgroup * 2 + slot) * BM * BN] (slot 0:
   // first segment, 1: last), which the reduce kernel adds in K order.
   int sk;
+  int sk_tiles;      // tiles in the split range (quarter = 1: 128 x 128 quarters of the 256 x 256
+                     // tiles from tile0 on, quarter t of tile tile0 + t / 4)
   int upt;           // K units per tile
   int ups;           // K steps (BK) per unit
   long long U;       // tiles * upt
@@ -149,7 +151,7 @@ void gemm_kernel(GemmParams P) {
   const int G = gridDim.x;
   int bid = blockIdx.x;
   int q = 0;
-  if (P.quarter) {
+  if (P.quarter && !P.sk) {
     q = bid & 3;
     bid >>= 2;
   } else if ((G & 7) == 0) {
@@ -157,7 +159,7 @@ void gemm_kernel(GemmParams P) {
   }
   // Tile id -> first row and column: a grouped row-major walk (kGroupM row tiles at a time, so a
   // group shares weight and activation blocks in L2).
-  const int tile_rows = P.sk ? BM : kTile, tile_cols = P.sk ? BN : kTile;
+  const int tile_rows = P.sk && !P.quarter ? BM : kTile, tile_cols = P.sk && !P.quarter ? BN : kTile;
   auto tile_origin = [&](int id, int* m0, int* n0) __attribute__((always_inline)) {
     const int per_group = kGroupM * P.tiles_n;
     const int group = id / per_group;
@@ -411,7 +413,12 @@ void gemm_kernel(GemmParams P) {
     const long long e = u1 < tb + P.upt ? u1 : tb + P.upt;
     const int kb = (int)(u - tb) * P.ups, ke = (int)(e - tb) * P.ups;
     int m0, n0;
-    tile_origin(t, &m0, &n0);
+    if (P.quarter) {
+      q = t & 3;
+      tile_origin(P.tile0 + (t >> 2), &m0, &n0);
+    } else {
+      tile_origin(t, &m0, &n0);
+    }
     run_segment(m0, n0, kb, ke);
     if (kb == 0 && ke == nk) {
       write_tile(m0, n0);
@@ -446,7 +453,7 @@ __global__ __launch_bounds__(kSkRedThreads) void gemm_sk_reduce_kernel(GemmParam
   const long long it = (long long)blockIdx.x * kSkRedThreads + threadIdx.x;
   const int t = (int)(it / C::kPartF4);
   const int e = (int)(it - (long long)t * C::kPartF4);
-  if (t >= P.tiles_m * P.tiles_n) return;
+  if (t >= P.sk_tiles) return;
   const long long tb = (long long)t * P.upt;
   const int lo = sk_owner(tb, P.U, G), hi = sk_owner(tb + P.upt - 1, P.U, G);
   if (lo == hi) return;  // one workgroup ran the whole tile and wrote it
@@ -459,13 +466,16 @@ __global__ __launch_bounds__(kSkRedThreads) void gemm_sk_reduce_kernel(GemmParam
                                                   rp, (slot * (uint32_t)C::kPartF4 + (uint32_t)e) * 16u, 0, 0));
     sum[0] += v[0]; sum[1] += v[1]; sum[2] += v[2]; sum[3] += v[3];
   }
-  // Tile origin (the same grouped walk as the main kernel).
+  // Tile origin (the same grouped walk as the main kernel; a quarter of a 256 x 256 tile when the
+  // split range is the quarters of a full-tile launch's last tiles).
+  const int id = P.quarter ? P.tile0 + (t >> 2) : t, qq = P.quarter ? t & 3 : 0;
+  const int tr = P.quarter ? kTile : BM, tc = P.quarter ? kTile : BN;
   const int per_group = kGroupM * P.tiles_n;
-  const int group = t / per_group;
+  const int group = id / per_group;
   const int first_m = group * kGroupM;
   const int gm = min(kGroupM, P.tiles_m - first_m);
-  const int in_group = t - group * per_group;
-  const int m0 = (first_m + in_group % gm) * BM, n0 = (in_group / gm) * BN;
+  const int in_group = id - group * per_group;
+  const int m0 = (first_m + in_group % gm) * tr + (qq >> 1) * BM, n0 = (in_group / gm) * tc + (qq & 1) * BN;
   int mi, ni;
   part_item_coords<C>(e, &mi, &ni);
   const int n = n0 + ni;
@@ -497,7 +507,7 @@ hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
 
 template <int BM, int BN>
 hipError_t launch_sk_reduce(const GemmParams& P, int G, hipStream_t stream) {
-  const long long items = (long long)P.tiles_m * P.tiles_n * GemmCfg<BM, BN>::kPartF4;
+  const long long items = (long long)P.sk_tiles * GemmCfg<BM, BN>::kPartF4;
   hipLaunchKernelGGL((gemm_sk_reduce_kernel<BM, BN>), dim3((unsigned)((items + kSkRedThreads - 1) / kSkRedThreads)),
                      dim3(kSkRedThreads), 0, stream, P, G);
   return hipGetLastError();
@@ -524,6 +534,15 @@ bool scale_rows_16b(const uint16_t* s, const uint16_t* b, int K) {
   return K % 512 == 0 && (reinterpret_cast<uintptr_t>(s) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0;
 }
 
+// Whole-tile launches: the 256 x 256 tiles of a last round that would leave more than half the CUs
+// idle, launched as 128 x 128 quarters after the others (0: none).
+int gemm_tail(int M, int N, int cus) {
+  const int c = cus > 0 ? cus : 1;
+  const int total = ((M + kTile - 1) / kTile) * ((N + kTile - 1) / kTile);
+  const int rem = total % c;
+  return (rem > 0 && 4 * rem <= 2 * c) ? rem : 0;
+}
+
 }  // namespace
 
 // More 128 x 128 tiles than CUs: whole rounds of 256 x 256 tiles (one per CU at a time) in one
@@ -536,6 +555,7 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   const int c = cus > 0 ? cus : 1;
   plan->sk = false;
   plan->sk256 = false;
+  plan->tail_sk = false;
   plan->G = 0;
   plan->part_bytes = 0;
   const long long tiles256 = (long long)((M + 255) / 256) * ((N + 255) / 256);
@@ -572,7 +592,23 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const bool sk = tiles <= c || (2 * tiles256 < c && 4 * tiles <= 5LL * c) ||
                   (M % 256 != 0 && tiles256 < c && tiles <= 2LL * c);
-  if (!sk) return true;
+  if (!sk) {
+    // A tail of fewer quarters than CUs: stream-K over the quarters (their K spread over every
+    // CU) instead of one quarter per workgroup on a few CUs.
+    const int tail = gemm_tail(M, N, c);
+    if (tail > 0 && 4 * tail < c && scale_rows_16b(s, b, K)) {
+      const long long Ut = 4LL * tail * (K / 512);
+      long long Gt = (long long)c * sk_occupancy(true);
+      if (Gt > Ut) Gt = Ut;
+      const size_t slot = (size_t)GemmCfg<128, 128>::kPartF4 * 16 * 2;
+      if ((size_t)Gt * slot <= ws_capacity && Gt >= 1) {
+        plan->tail_sk = true;
+        plan->G = (int)Gt;
+        plan->part_bytes = (size_t)Gt * slot;
+      }
+    }
+    return true;
+  }
   const bool sb8 = scale_rows_16b(s, b, K);
   const int ups = sb8 ? 8 : 2;
   const long long U = tiles * (K / BK / ups);
@@ -592,7 +628,7 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
   GemmParams P;
   P.x = x; P.w = w; P.s = s; P.b = b; P.y = y;
   P.M = M; P.N = N; P.K = K;
-  P.sk = 0; P.upt = 0; P.ups = 0; P.U = 0; P.part = part;
+  P.sk = 0; P.sk_tiles = 0; P.upt = 0; P.ups = 0; P.U = 0; P.part = part;
   // 16-byte loads of 8 groups need 16-byte aligned scale rows and pointers.
   const bool sb8 = scale_rows_16b(s, b, K);
   if (plan.sk256) {
@@ -604,7 +640,8 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
     P.sk = 1;
     P.ups = 8;
     P.upt = K / BK / P.ups;
-    P.U = (long long)P.tiles_m * P.tiles_n * P.upt;
+    P.sk_tiles = P.tiles_m * P.tiles_n;
+    P.U = (long long)P.sk_tiles * P.upt;
     hipError_t e = launch_tiles<256, 256, true>(P, plan.G, stream);
     if (e != hipSuccess) return e;
     return launch_sk_reduce<256, 256>(P, plan.G, stream);
@@ -617,7 +654,8 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
     P.sk = 1;
     P.ups = sb8 ? 8 : 2;
     P.upt = K / BK / P.ups;
-    P.U = (long long)P.tiles_m * P.tiles_n * P.upt;
+    P.sk_tiles = P.tiles_m * P.tiles_n;
+    P.U = (long long)P.sk_tiles * P.upt;
     hipError_t e = sb8 ? launch_tiles<128, 128, true, kSkRing>(P, plan.G, stream)
                        : launch_tiles<128, 128, false>(P, plan.G, stream);
     if (e != hipSuccess) return e;
@@ -625,17 +663,27 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
   }
   P.tiles_m = (M + kTile - 1) / kTile;
   P.tiles_n = (N + kTile - 1) / kTile;
-  const int total = P.tiles_m * P.tiles_n;
-  const int c = cus > 0 ? cus : 1;
-  const int rem = total % c;
-  const int tail = (rem > 0 && 4 * rem <= 2 * c) ? rem : 0;
-  const int main_tiles = total - tail;
+  const int main_tiles = P.tiles_m * P.tiles_n - gemm_tail(M, N, cus);
+  const int tail = P.tiles_m * P.tiles_n - main_tiles;
   if (main_tiles > 0) {
     P.tile0 = 0;
     P.quarter = 0;
     hipError_t e = sb8 ? launch_tiles<256, 256, true>(P, main_tiles, stream)
                        : launch_tiles<256, 256, false>(P, main_tiles, stream);
     if (e != hipSuccess) return e;
+  }
+  if (tail > 0 && plan.tail_sk) {
+    if (!sb8) return hipErrorInvalidValue;
+    P.tile0 = main_tiles;
+    P.quarter = 1;
+    P.sk = 1;
+    P.ups = 8;
+    P.upt = K / BK / P.ups;
+    P.sk_tiles = 4 * tail;
+    P.U = (long long)P.sk_tiles * P.upt;
+    hipError_t e = launch_tiles<128, 128, true, kSkRing>(P, plan.G, stream);
+    if (e != hipSuccess) return e;
+    return launch_sk_reduce<128, 128>(P, plan.G, stream);
   }
   if (tail > 0) {
     P.tile0 = main_tiles;

@@ -139,7 +139,8 @@ hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 struct GemmPlan {
   bool sk;            // stream-K
   bool sk256;         // stream-K over 256 x 256 tiles (else 128 x 128)
-  int G;              // stream-K workgroups
+  bool tail_sk;       // whole tiles whose quarter-tile tail runs as stream-K over the quarters
+  int G;              // stream-K workgroups (of the whole launch, or of the tail)
   size_t part_bytes;  // stream-K partial tiles (two per workgroup)
 };
 // `ws_capacity`: the most partial-tile bytes the caller's workspace can hold (stream-K spreads

@@ -156,6 +156,13 @@ void check_gemm(int M, int N, int K, int cus) {
       GP(p.part_bytes == (size_t)p.G * t * t * 4 * 2);
       GP(p.part_bytes <= cap);
       if (p.sk256) GP(K % 512 == 0 && M >= 256 && p.G == cus);  // 8-step units, one workgroup per CU
+    } else if (p.tail_sk) {
+      // Whole tiles whose last round (fewer quarters than CUs) runs as stream-K over its quarters.
+      const long long total = (long long)((M + 255) / 256) * ((N + 255) / 256);
+      const long long rem = total % cus;
+      GP(K % 512 == 0 && rem > 0 && 4 * rem < cus && !p.sk256);
+      GP(p.G >= 1 && p.G <= 4 * rem * (K / 512));
+      GP(p.part_bytes == (size_t)p.G * 128 * 128 * 4 * 2 && p.part_bytes <= cap);
     } else {
       GP(!p.sk256 && p.part_bytes == 0);
     }
