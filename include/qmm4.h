@@ -68,7 +68,10 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
  * y = x @ dequant(w)^T without any allocation: the same checks, kernels and results (bit for bit)
  * as qmm4_affine_bf16, with the split-K workspace in a static device array of
  * QMM4_NOALLOC_SCRATCH_BYTES per GPU (64 KiB of counters, the rest fp32 partial sums) instead of a
- * library allocation. It has no counterpart in the reference: it is for callers that cannot
+ * library allocation. The array holds the largest workspace any plan takes on a 256-CU MI355X (the
+ * GEMM's stream-K over 256 x 256 tiles: 256 workgroups x two 256 KiB partial tiles), so every
+ * shape gets the plan qmm4_affine_bf16 takes; on a GPU with more CUs a plan that would not fit
+ * falls back to one that does (results then within the parity tolerance, not bit for bit). It has no counterpart in the reference: it is for callers that cannot
  * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
  *   - Calls no hipMalloc / hipFree / allocating routine. The first call on a device looks the array
  *     up and clears its counters on `hip_stream` (that call must not be captured:
@@ -77,7 +80,7 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
  *   - Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different
  *     streams, or threads without ordering between them) race. Order them on one stream.
  */
-#define QMM4_NOALLOC_SCRATCH_BYTES (32u * 1024u * 1024u)
+#define QMM4_NOALLOC_SCRATCH_BYTES (136u * 1024u * 1024u)
 int qmm4_affine_bf16_noalloc(const void* x, const uint32_t* w, const void* scales, const void* biases,
                              void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
                              int transpose, void* hip_stream);

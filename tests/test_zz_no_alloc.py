@@ -31,13 +31,17 @@ def run(fn, x, w, s, b, m, n, k, stream):
 
 # (larger shape, smaller shape) per kernel family that takes a split-K workspace: row-split with K
 # slices (counters + partials), row-phase with a K split (partials), K-split verify (counters +
-# partials), stream-K skinny (counters + partials); and a GEMM shape (no workspace).
+# partials), stream-K skinny (counters + partials); the GEMM's stream-K over 128 x 128 tiles on a
+# few and on 256 workgroups (32 MiB of partials); its stream-K over 256 x 256 tiles (128 MiB of
+# partials, the largest workspace) and over the quarters of a last round of whole tiles.
 PAIRS = [
     ((2, 5120, 17408), (1, 2048, 8192)),
     ((64, 5120, 17408), (24, 2048, 5120)),
     ((16, 512, 5120), (8, 256, 2048)),
     ((3, 256, 4096), (2, 64, 1024)),
     ((96, 512, 1024), (80, 256, 512)),
+    ((512, 5120, 17408), (128, 17408, 5120)),
+    ((1024, 17408, 5120), (96, 512, 1024)),
 ]
 
 
