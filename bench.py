@@ -325,7 +325,7 @@ def measure_layer_tail(torch, dev, rows_list=(4, 64), n_layers: int = 2, samples
     return out
 
 
-def measure_rows(torch, lib, dev, samples: int, table: dict) -> dict:
+def measure_rows(torch, lib, dev, samples: int, table: dict, floors: dict | None = None) -> dict:
     """Per-call medians (HIP events per launch, rotating weight copies) of each shape of `table` at
     its row counts, with HBM and bf16-MFMA fractions of peak: the up and down projections at 65 to
     2048 rows (MID), every linear and head of the model at decode and verify rows (MODEL)."""
@@ -341,6 +341,8 @@ def measure_rows(torch, lib, dev, samples: int, table: dict) -> dict:
             out[f"{name} M={m}"] = {"shape": f"{m}x{wl.k}->{wl.n}", "us": round(med * 1e6, 2),
                                     "hbm_frac": round(hf, 4), "mfma_frac": round(mf, 4),
                                     "max_frac": round(max(hf, mf), 4), "samples": len(ts)}
+            if floors is not None:
+                attach_floor(out[f"{name} M={m}"], byt, med * 1e6, floors, f"{floors['cus']}x1024")
             log(f"[bench]   {name} M={m}: {med * 1e6:8.2f} us  HBM {hf:.1%}  MFMA {mf:.1%}")
         del wl
         torch.cuda.empty_cache()
@@ -403,6 +405,93 @@ def time_launches(torch, wl: Workload, m: int, samples: int) -> list[float]:
         b.record()
     torch.cuda.synchronize()
     return [a.elapsed_time(b) * 1e-3 for a, b in evs]
+
+
+def load_floor_lib():
+    """libqmm4_floor.so (built beside libqmm4.so by build()): an empty kernel and a streaming read."""
+    import ctypes
+
+    from mlx_tree_spec_amd import build as kbuild
+
+    lib = ctypes.CDLL(kbuild.FLOOR_PATH)
+    lib.qmm4_floor_empty.restype = ctypes.c_int
+    lib.qmm4_floor_empty.argtypes = [ctypes.c_int, ctypes.c_int, ctypes.c_int, ctypes.c_void_p]
+    lib.qmm4_floor_read.restype = ctypes.c_int
+    lib.qmm4_floor_read.argtypes = [ctypes.c_void_p, ctypes.c_uint64, ctypes.c_void_p, ctypes.c_int, ctypes.c_void_p]
+    return lib
+
+
+def measure_floors(torch, dev, samples: int = 30) -> dict:
+    """What one GPU can do at best, timed the way the workloads are (HIP events per launch, after a
+    warm-up): an empty kernel launched with the grids the quantized-matmul kernels use (one
+    workgroup per CU of 1024 or 512 threads; four per CU), a 512 MiB device-to-device copy
+    (torch's, read + write bytes: `hbm_ceiling_gbs`), and a 1 GiB streaming read by a plain kernel
+    (16-byte loads, four in flight per thread: `hbm_read_ceiling_gbs`, the pattern of the weight
+    streams). Each HBM-bound workload is then reported against `hbm_read_ceiling_gbs` and against
+    a floor of one empty launch plus its bytes at that rate."""
+    fl = load_floor_lib()
+    stream = torch.cuda.current_stream(dev).cuda_stream
+    cus = torch.cuda.get_device_properties(dev).multi_processor_count
+
+    def event_times(fn, n):
+        evs = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)) for _ in range(n)]
+        for a, b in evs:
+            a.record()
+            fn()
+            b.record()
+        torch.cuda.synchronize()
+        return [a.elapsed_time(b) * 1e-3 for a, b in evs]
+
+    def check(rc, what):
+        if rc != 0:
+            raise RuntimeError(f"{what} failed (hipError {rc})")
+
+    out = {"cus": cus, "empty_launch_us": {}}
+    for blocks, threads in ((cus, 1024), (cus, 512), (4 * cus, 256)):
+        fn = lambda: check(fl.qmm4_floor_empty(blocks, threads, 0, stream), "empty launch")
+        for _ in range(200):
+            fn()
+        med = statistics.median(event_times(fn, samples))
+        out["empty_launch_us"][f"{blocks}x{threads}"] = round(med * 1e6, 2)
+        log(f"[bench]   empty launch {blocks} x {threads}: {med * 1e6:6.2f} us")
+    n = (512 << 20) // 4
+    src = torch.empty(n, dtype=torch.int32, device=dev)
+    dst = torch.empty_like(src)
+    src.fill_(7)
+    for _ in range(5):
+        dst.copy_(src)
+    med = statistics.median(event_times(lambda: dst.copy_(src), samples))
+    out["hbm_ceiling_gbs"] = round(2 * src.numel() * 4 / med / 1e9, 1)
+    out["copy"] = {"bytes": 2 * src.numel() * 4, "us": round(med * 1e6, 2), "what": "torch copy_ of 512 MiB, read + write"}
+    log(f"[bench]   512 MiB device-to-device copy: {med * 1e6:8.1f} us  {out['hbm_ceiling_gbs']:7.1f} GB/s (read + write)")
+    del src, dst
+    rb = 1 << 30
+    buf = torch.empty(rb // 4, dtype=torch.int32, device=dev)
+    buf.fill_(3)
+    blocks = 8 * cus
+    sink = torch.zeros(blocks * 4, dtype=torch.int32, device=dev)
+    fn = lambda: check(fl.qmm4_floor_read(buf.data_ptr(), rb, sink.data_ptr(), blocks, stream), "streaming read")
+    for _ in range(5):
+        fn()
+    med = statistics.median(event_times(fn, samples))
+    out["hbm_read_ceiling_gbs"] = round(rb / med / 1e9, 1)
+    out["read"] = {"bytes": rb, "us": round(med * 1e6, 2), "workgroups": blocks,
+                   "what": "plain kernel, 16-byte loads, 4 in flight per thread"}
+    log(f"[bench]   1 GiB streaming read: {med * 1e6:8.1f} us  {out['hbm_read_ceiling_gbs']:7.1f} GB/s")
+    del buf, sink
+    torch.cuda.empty_cache()
+    return out
+
+
+def attach_floor(entry: dict, byt: int, us: float, floors: dict, empty_key: str) -> None:
+    """Adds the workload's fraction of the measured read ceiling and its achievable floor (one empty
+    launch of the kernel's grid plus its algorithmic bytes at the read ceiling)."""
+    rc = floors["hbm_read_ceiling_gbs"]
+    empty = floors["empty_launch_us"][empty_key]
+    floor_us = empty + byt / (rc * 1e9) * 1e6
+    entry["ceiling_frac"] = round(byt / (us * 1e-6) / 1e9 / rc, 4)
+    entry["floor_us"] = round(floor_us, 2)
+    entry["floor_frac"] = round(floor_us / us, 4)
 
 
 def cpu_baseline(wl_rows, k, n, budget_s: float = 10.0) -> dict:
@@ -517,6 +606,10 @@ def main() -> int:
     if "c1" not in only:
         only = ["c1"] + only
 
+    log("[bench] floors: empty launches, HBM copy and streaming-read ceilings")
+    floors = measure_floors(torch, dev, args.samples)
+    empty_key = f"{floors['cus']}x1024"
+
     out_workloads = {}
     head = None
     for name in only:
@@ -534,7 +627,9 @@ def main() -> int:
                 "hbm_frac": round(byt / med / 1e9 / HBM_PEAK_GBS, 4),
                 "tflops": round(fl / med / 1e12, 2), "mfma_frac": round(fl / med / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
                 "bytes": byt, "flops": fl, "samples": len(ts)}
-            log(f"[bench]   M={m}: {med * 1e6:8.2f} us  {byt / med / 1e9:7.1f} GB/s  {fl / med / 1e12:7.1f} TFLOP/s")
+            attach_floor(res["per_m"][str(m)], byt, med * 1e6, floors, empty_key)
+            log(f"[bench]   M={m}: {med * 1e6:8.2f} us  {byt / med / 1e9:7.1f} GB/s  {fl / med / 1e12:7.1f} TFLOP/s"
+                f"  (floor {res['per_m'][str(m)]['floor_us']:.2f} us)")
         out_workloads[name] = res
         if name == "c1":
             head = (wl, res)
@@ -546,11 +641,11 @@ def main() -> int:
     mid = {}
     if not args.no_mid:
         log("[bench] mid-size M: up and down projections at 65 to 2048 rows")
-        mid = measure_rows(torch, lib, dev, args.samples, MID)
+        mid = measure_rows(torch, lib, dev, args.samples, MID, floors)
     model = {}
     if not args.no_model:
         log("[bench] the model's linears and heads at decode and verify rows")
-        model = measure_rows(torch, lib, dev, args.samples, MODEL)
+        model = measure_rows(torch, lib, dev, args.samples, MODEL, floors)
     log("[bench] one GPU's share of an 8-way column split")
     shard8 = measure_shard8(torch, lib, dev, args.samples)
     log("[bench] fused ops either side of the projection")
@@ -602,6 +697,9 @@ def main() -> int:
                    "weight_copies": wl.copies},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": prof["traffic"],
+                     "frac_step": round(value / HBM_PEAK_GBS, 4),
+                     "hbm_ceiling": floors["hbm_ceiling_gbs"], "hbm_read_ceiling": floors["hbm_read_ceiling_gbs"],
+                     "frac_of_read_ceiling": round(achieved / floors["hbm_read_ceiling_gbs"], 4),
                      "kernel": f"qmm4::{HEAD_KERNEL} (rows <= 4, one workgroup per CU owning 136 weight rows)",
                      "mean_launch_us": round(statistics.mean(durs) * 1e6, 3),
                      "bytes_per_launch": round(mean_bytes),
@@ -609,9 +707,13 @@ def main() -> int:
                      "event_overhead_us": (round(statistics.mean(durs) * 1e6 - prof["trace_mean_us"], 3)
                                            if prof["trace_mean_us"] else None),
                      "note": "achieved/frac: HIP events around each launch on the launch stream (they include "
-                             "the dispatch); trace_mean_us/frac_trace: the kernel's average duration in the "
+                             "the dispatch); frac_step: the timed steps' value over the peak; "
+                             "trace_mean_us/frac_trace: the kernel's average duration in the "
                              "committed rocprofv3 kernel trace of the default bench run; traffic: the committed "
-                             "FETCH_SIZE/WRITE_SIZE passes, null unless they name this kernel"},
+                             "FETCH_SIZE/WRITE_SIZE passes, null unless they name this kernel; hbm_ceiling: a "
+                             "512 MiB device-to-device copy in this run (read + write bytes); hbm_read_ceiling: "
+                             "a plain streaming-read kernel over 1 GiB in this run"},
+        "floors": floors,
         "workloads": out_workloads,
         "mid_m": mid,
         "model_linears": model,

@@ -70,12 +70,14 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
  * QMM4_NOALLOC_SCRATCH_BYTES per GPU (64 KiB of counters, the rest fp32 partial sums) instead of a
  * library allocation. The array holds the largest workspace any plan takes on a 256-CU MI355X (the
  * GEMM's stream-K over 256 x 256 tiles: 256 workgroups x two 256 KiB partial tiles), so every
- * shape gets the plan qmm4_affine_bf16 takes; on a GPU with more CUs a plan that would not fit
- * falls back to one that does (results then within the parity tolerance, not bit for bit). It has no counterpart in the reference: it is for callers that cannot
- * allocate (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc).
+ * shape whose arrival counters fit in 64 KiB gets the plan qmm4_affine_bf16 takes; on a GPU with
+ * more CUs a plan that would not fit falls back to one that does (results then within the parity
+ * tolerance, not bit for bit). It has no counterpart in the reference: it is for callers that
+ * cannot allocate (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).
  *   - Calls no hipMalloc / hipFree / allocating routine. The first call on a device looks the array
- *     up and clears its counters on `hip_stream` (that call must not be captured:
- *     QMM4_ERR_CAPTURE); later calls on that device may be captured.
+ *     up, clears its counters on `hip_stream` and waits for that clear (that call must not be
+ *     captured: QMM4_ERR_CAPTURE); later calls on that device may be captured.
  *   - A shape whose split-K buffers exceed the array returns QMM4_ERR_INVALID with the sizes.
  *   - Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different
  *     streams, or threads without ordering between them) race. Order them on one stream.

@@ -58,6 +58,10 @@ int device_scratch(int dev, hipStream_t stream, uint8_t** out) {
   if (e != hipSuccess) return hip_error(e, "hipGetSymbolAddress(scratch)");
   e = launch_zero_u32(static_cast<uint32_t*>(p), kNoallocCounterBytes / sizeof(uint32_t), stream);
   if (e != hipSuccess) return hip_error(e, "static scratch counter clear");
+  // The pointer is published only once the clear has finished, so a later call on another
+  // stream cannot read counters that are not yet zero (this call is not captured: see above).
+  e = hipStreamSynchronize(stream);
+  if (e != hipSuccess) return hip_error(e, "static scratch counter clear (synchronize)");
   ptrs.emplace(dev, static_cast<uint8_t*>(p));
   *out = static_cast<uint8_t*>(p);
   return QMM4_OK;

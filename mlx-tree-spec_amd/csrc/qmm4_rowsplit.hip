@@ -144,7 +144,7 @@ template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, int PAI
 __global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
 void rowsplit_kernel(RowSplitParams P) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "x rows per fragment");
-  static_assert(!SMALL || (!FUSED && !KSPLIT), "small plans are plain whole-K projections");
+  static_assert(!SMALL || (!FUSED && !KSPLIT && !NORM), "small plans are plain whole-K projections of 6+ rows");
   static_assert(!PAIR || (!FUSED && !KSPLIT && !SMALL && !NORM), "paired units are plain whole-K projections");
   static_assert(!OWN || (!FUSED && !KSPLIT && !SMALL && !NORM && !PAIR && V == 4), "own blocks: plain whole-K projections");
   static_assert(!NORM || (MP == 4 && kRsThreads == MP * kRsNormThreads), "one thread group per normalised row");
@@ -977,8 +977,12 @@ hipError_t launch_rowsplit_k(const RowSplitPlan& plan, const RowSplitParams& P, 
 
 template <int MP, bool NORM>
 hipError_t launch_rowsplit_m(const RowSplitPlan& plan, const RowSplitParams& P, hipStream_t stream) {
-  if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true, NORM>(plan, P, stream);
-  if constexpr (!NORM) {
+  if constexpr (NORM) {
+    // The normalising staging runs with the regular forms only (rowsplit_norm_ok: 4-row
+    // fragments, while the SMALL form starts at 6 rows).
+    if (plan.small || plan.pair || plan.own) return hipErrorInvalidValue;
+  } else {
+    if (plan.small) return launch_rowsplit_t<MP, 4, false, false, true, false>(plan, P, stream);
     if (plan.pair)
       return plan.GU == 2 ? launch_rowsplit_t<MP, 4, false, false, false, false, 1>(plan, P, stream)
                           : launch_rowsplit_t<MP, 4, false, false, false, false, 2>(plan, P, stream);
@@ -997,7 +1001,7 @@ hipError_t launch_rowsplit_xreg(const RowSplitPlan& plan, const RowSplitParams& 
 }
 
 bool rowsplit_norm_ok(const RowSplitPlan& plan, int M, int K) {
-  return !plan.xreg && !plan.pair && !plan.own && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
+  return !plan.xreg && !plan.small && !plan.pair && !plan.own && plan.MP == 4 && M >= 1 && M <= 4 && K % 8 == 0 &&
          K <= kRsNormThreads * kRsNormChunks * 8 && rowsplit_smem(plan, true) <= kRsLds;
 }
 

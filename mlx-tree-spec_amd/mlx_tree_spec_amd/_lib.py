@@ -21,6 +21,9 @@ QMM4_ERR_CAPTURE = -16
 QMM4_EPILOGUE_NONE = 0
 QMM4_EPILOGUE_SILU_MUL = 1
 
+# Size of qmm4_affine_bf16_noalloc's static device array per GPU (QMM4_NOALLOC_SCRATCH_BYTES).
+QMM4_NOALLOC_SCRATCH_BYTES = 136 * 1024 * 1024
+
 # name -> (restype, argtypes); the symbols include/qmm4.h declares.
 _vp = ctypes.c_void_p
 _i64 = ctypes.c_int64

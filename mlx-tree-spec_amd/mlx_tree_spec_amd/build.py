@@ -21,6 +21,10 @@ CSRC = os.path.join(PROJ_DIR, "csrc")
 INCLUDE = os.path.join(REPO_DIR, "include")
 LIB_NAME = "libqmm4.so"
 LIB_PATH = os.path.join(PKG_DIR, LIB_NAME)
+# The benchmark's measurement floors (an empty launch, a streaming read): csrc/floor/, a library
+# of its own that only bench.py loads.
+FLOOR_DIR = os.path.join(CSRC, "floor")
+FLOOR_PATH = os.path.join(PKG_DIR, "libqmm4_floor.so")
 ARCH = os.environ.get("QMM4_OFFLOAD_ARCH", "gfx950")
 
 # -packed-fp32-ops off: no v_pk_{add,mul,fma}_f32 in device code. hipcc's host pass warns that
@@ -43,21 +47,25 @@ def _compile(src: str, obj: str) -> None:
         raise RuntimeError(f"hipcc failed for {src}:\n{r.stdout}\n{r.stderr}")
 
 
-def build(verbose: bool = False) -> str:
-    srcs = sources()
+def _link(srcs: list[str], out: str) -> None:
     with tempfile.TemporaryDirectory(prefix="qmm4_build_") as tmp:
         objs = [os.path.join(tmp, os.path.basename(s) + ".o") for s in srcs]
         with cf.ThreadPoolExecutor(max_workers=min(8, len(srcs))) as ex:
             list(ex.map(_compile, srcs, objs))
-        out_tmp = LIB_PATH + f".tmp{os.getpid()}"
+        out_tmp = out + f".tmp{os.getpid()}"
         # --no-undefined: a kernel whose host stub the compiler dropped fails here, not at load time.
         cmd = ["hipcc", f"--offload-arch={ARCH}", "-shared", "-fPIC", "-Wl,--no-undefined", *objs, "-o", out_tmp]
         r = subprocess.run(cmd, capture_output=True, text=True)
         if r.returncode != 0:
             raise RuntimeError(f"link failed:\n{r.stdout}\n{r.stderr}")
-        os.replace(out_tmp, LIB_PATH)
+        os.replace(out_tmp, out)
+
+
+def build(verbose: bool = False) -> str:
+    _link(sources(), LIB_PATH)
+    _link(sorted(os.path.join(FLOOR_DIR, f) for f in os.listdir(FLOOR_DIR) if f.endswith(".hip")), FLOOR_PATH)
     if verbose:
-        print(f"built {LIB_PATH}")
+        print(f"built {LIB_PATH} and {FLOOR_PATH}")
     return LIB_PATH
 
 

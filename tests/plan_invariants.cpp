@@ -6,6 +6,7 @@
 // tests/test_plans.py; no GPU is touched.
 #include <cstdio>
 #include <cstdint>
+#include <string>
 
 #include "qmm4_kernels.h"
 
@@ -172,7 +173,51 @@ void check_gemm(int M, int N, int K, int cus) {
 
 }  // namespace
 
-int main() {
+// Query mode (`plan_invariants query`): one shape per stdin line, "<planner> M N K cus", with
+// planner rowsplit, rowsplit_fused, xreg, rowphase or gemm; prints one line per query with the
+// plan's form ("none" when the planner declines), so tests can check which form a GPU test case
+// reaches on a given CU count.
+int query() {
+  char kind[32];
+  int M, N, K, cus;
+  while (std::scanf("%31s %d %d %d %d", kind, &M, &N, &K, &cus) == 5) {
+    const std::string k = kind;
+    if (k == "rowsplit" || k == "rowsplit_fused") {
+      RowSplitPlan p{};
+      if (!rowsplit_plan(M, N, K, cus, k == "rowsplit_fused", &p)) {
+        std::printf("none\n");
+        continue;
+      }
+      std::printf("MP=%d KS=%d V=%d small=%d pair=%d own=%d norm_ok=%d blocks=%d\n", p.MP, p.KS, p.V, (int)p.small,
+                  (int)p.pair, (int)p.own, (int)rowsplit_norm_ok(p, M, K), p.blocks);
+    } else if (k == "xreg") {
+      RowSplitPlan p{};
+      std::printf(rowsplit_xreg_plan(M, N, K, cus, &p) ? "xreg blocks=%d\n" : "none\n", p.blocks);
+    } else if (k == "rowphase") {
+      RowPhasePlan p{};
+      if (!rowphase_plan(M, N, K, cus, &p)) {
+        std::printf("none\n");
+        continue;
+      }
+      std::printf("variant=%d S=%d wide=%d blocks=%d\n", p.variant, p.S, (int)p.wide, p.blocks);
+    } else if (k == "gemm") {
+      const uint16_t* s = reinterpret_cast<const uint16_t*>(uintptr_t{0x100000});
+      const uint16_t* b = reinterpret_cast<const uint16_t*>(uintptr_t{0x200000});
+      GemmPlan p{};
+      if (!gemm_plan(M, N, K, cus, (size_t)1 << 34, s, b, &p)) {
+        std::printf("none\n");
+        continue;
+      }
+      std::printf("sk=%d sk256=%d tail_sk=%d G=%d\n", (int)p.sk, (int)p.sk256, (int)p.tail_sk, p.G);
+    } else {
+      std::printf("unknown\n");
+    }
+  }
+  return 0;
+}
+
+int main(int argc, char** argv) {
+  if (argc > 1 && std::string(argv[1]) == "query") return query();
   const int Ms[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16, 17, 24, 32, 33, 48, 63, 64, 65, 128, 300, 1024, 4096};
   const int Ns[] = {16, 32, 48, 256, 1024, 1040, 2048, 3072, 4096, 4112, 5120, 6144, 10240, 12288,
                     17408, 34816, 65984, 131072, 151936, 248320, 248336, 262144};

@@ -1,0 +1,58 @@
+"""GPU test shapes whose kernel route is the point of the test, with the route each takes on a
+256-CU MI355X.
+
+The GPU tests (test_gpu_norm_fold.py, test_gpu_mlp.py) parametrize over these lists, and
+tests/test_plans.py checks every label against the built planners on the CPU, so a planner retune
+that moves a case off its route fails there instead of silently dropping the coverage.
+
+Routes of the residual add + RMS norm folded into the projection (qmm4_add_rms_norm_qmm_bf16):
+  "fold KS=1"     one row-split launch over whole K, x normalised as it is staged;
+  "fold KS=2"     the same with K in 2 slices (each slice stages its own part of the normalised
+                  row; the slices' sums meet through the arrival counters);
+  "two launches"  the norm kernel, then the projection on its n (more than 4 rows, K above the
+                  folded 8192, or a row-split plan that cannot normalise while staging).
+Routes of the gate+up SiLU·mul projection (qmm4_gate_up_silu_bf16):
+  "fused"     one row-split launch with the epilogue fused;
+  "two-pass"  the projection into the library's scratch, then the SiLU·mul pass (no fused
+              row-split plan: more than 16 rows, or an x slice too large for LDS).
+"""
+
+CUS = 256
+
+# (M, N, K, silu_mul, route)
+FOLD_CASES = [
+    (1, 34816, 5120, True, "fold KS=1"),    # decode gate+up (the decode MLP's first projection)
+    (2, 34816, 5120, True, "fold KS=1"),
+    (4, 34816, 5120, True, "fold KS=1"),
+    (1, 17408, 5120, False, "fold KS=1"),   # plain
+    (3, 5120, 5120, False, "fold KS=1"),    # one or two 16-row blocks per CU
+    (4, 5120, 512, False, "fold KS=1"),     # one unit per block
+    (2, 20480, 640, False, "fold KS=1"),    # units of 5 super-steps
+    (2, 12288, 8192, False, "fold KS=1"),   # the largest folded K (4 chunks per thread)
+    (1, 94240, 8192, True, "fold KS=2"),    # gate+up: whole-K unit slots exceed LDS
+    (1, 176160, 6400, False, "fold KS=2"),  # plain, units of 5 super-steps (no paired form)
+    (5, 5120, 5120, False, "two launches"),  # 5 rows: norm kernel + row-split (8-row fragments)
+    (4, 5120, 10240, False, "two launches"),  # K > 8192
+    (16, 8192, 1024, True, "two launches"),  # 16 rows: norm kernel + fused gate+up (K in 2 slices)
+]
+
+# (M, K, N, route): gate+up weights [N, K] stacked as [gate; up].
+GATE_UP_CASES = [
+    (1, 5120, 34816, "fused"),
+    (2, 5120, 34816, "fused"),
+    (4, 5120, 34816, "fused"),
+    (3, 4096, 34848, "fused"),    # 17424 = 242 x 72: a partial last range
+    (4, 17408, 10240, "fused"),
+    (9, 5120, 34816, "fused"),    # 9-16 rows: 16-row fragments, K in slices
+    (12, 5120, 34816, "fused"),
+    (16, 5120, 34816, "fused"),
+    (16, 5120, 20480, "fused"),
+    (1, 512, 256, "fused"),       # one block per workgroup
+    (5, 2048, 4096, "fused"),
+    (16, 1024, 2048, "fused"),
+    (1, 81920, 32, "two-pass"),   # x slices too large for LDS at every K split
+    (3, 81920, 256, "two-pass"),
+    (16, 20480, 1024, "two-pass"),
+    (64, 5120, 1024, "two-pass"),  # row-phase underneath
+    (100, 512, 4096, "two-pass"),  # GEMM underneath
+]

@@ -25,6 +25,16 @@ def test_header_declares_expected_api():
                                            "qmm4_add_rms_norm_qmm_bf16", "qmm4_last_error", "qmm4_abi_version"])
 
 
+def test_constants_match_the_header():
+    src = re.sub(r"/\*.*?\*/", "", open(HEADER).read(), flags=re.S)
+    defines = {k: v for k, v in re.findall(r"^#define\s+(QMM4_\w+)\s+(.+?)\s*$", src, flags=re.M)}
+    for name in ("QMM4_OK", "QMM4_ERR_INVALID", "QMM4_ERR_UNSUPPORTED", "QMM4_ERR_NOMEM", "QMM4_ERR_HIP",
+                 "QMM4_ERR_CAPTURE", "QMM4_EPILOGUE_NONE", "QMM4_EPILOGUE_SILU_MUL", "QMM4_NOALLOC_SCRATCH_BYTES"):
+        assert name in defines, name
+        value = eval(defines[name].replace("u", ""), {})  # integer literals and products
+        assert getattr(_lib, name) == value, (name, defines[name])
+
+
 def test_library_exports_every_declared_symbol():
     lib = _lib.load()
     for name in declared_functions():

@@ -14,6 +14,7 @@ import torch
 from mlx_tree_spec_amd import STATS, QuantizedLinear, QuantizedMLP, gate_up_silu, quantized_matmul
 from oracle import cpu
 from oracle import qmm4_oracle as O
+from route_cases import GATE_UP_CASES
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -59,23 +60,15 @@ def check_gate_up(x, w, s, b):
     return y
 
 
-# Up to 16 rows over a large N: one row-split launch with the epilogue fused. N = 34848 leaves the
-# last workgroup a partial range (17424 = 242 x 72); K = 4096 gives units of 4 super-steps, 5120 of 5.
-# 9 to 16 rows (a tree-verify batch) take 16-row fragments with K in slices.
-@pytest.mark.parametrize("m,k,n", [(1, 5120, 34816), (2, 5120, 34816), (4, 5120, 34816), (3, 4096, 34848),
-                                   (4, 17408, 10240), (9, 5120, 34816), (12, 5120, 34816), (16, 5120, 34816),
-                                   (16, 5120, 20480)])
-def test_gate_up_silu_fused_rowsplit(m, k, n):
+# One row-split launch with the epilogue fused (up to 16 rows; N = 34848 leaves the last workgroup a
+# partial range, K = 4096 gives units of 4 super-steps, 5120 of 5, 9 to 16 rows take 16-row
+# fragments with K in slices), or the projection into the library's scratch buffer followed by the
+# epilogue pass (x slices too large for LDS at up to 16 rows; the row-phase and GEMM kernels
+# underneath at 64 and 100 rows). tests/test_plans.py checks each case's route against the planner.
+@pytest.mark.parametrize("m,k,n,route", GATE_UP_CASES)
+def test_gate_up_silu(m, k, n, route):
+    print(f"  gate_up M={m} K={k} N={n} ({route})", flush=True)
     x, w, s, b = O.make_inputs(m, k, n, seed=m + 31 * k + n)
-    check_gate_up(x, w, s, b)
-
-
-# Other shapes: the projection into the library's scratch buffer, then the epilogue pass (verify,
-# row-phase, skinny and GEMM kernels underneath).
-@pytest.mark.parametrize("m,k,n", [(1, 512, 256), (5, 2048, 4096), (16, 1024, 2048), (64, 5120, 1024),
-                                   (100, 512, 4096)])
-def test_gate_up_silu_two_pass(m, k, n):
-    x, w, s, b = O.make_inputs(m, k, n, seed=m + 17 * k + n)
     check_gate_up(x, w, s, b)
 
 

@@ -9,9 +9,10 @@ qmm4_add_rms_norm_qmm_bf16 replaces the pair add_rms_norm + projection of tree_v
   - against the oracle: h bit-exact; n at least 99.9% bit-equal and every value within two bf16
     ulps (the fp32 row sum's order is the kernel's own); y to max_rel <= 1e-2, mean_rel <= 2e-3
     of the oracle's fp32-accumulated projection (and SiLU·mul) of the GPU's n.
-The shapes cover each form of the folded kernel (whole K, K slices, the small form, units of 4
-and 5 super-steps, the plain and the gate+up epilogue, K from 512 to the largest folded 8192) and
-the shapes that run as two launches (5 rows, K > 8192, 16 rows with the two-pass gate+up).
+The shapes (route_cases.FOLD_CASES, whose routes tests/test_plans.py checks against the planner)
+cover each form of the folded kernel (whole K, K in 2 slices for the plain and the gate+up
+epilogue, units of 4 and 5 super-steps, K from 512 to the largest folded 8192) and the shapes that
+run as two launches (5 rows, K > 8192, 16 rows).
 """
 
 import numpy as np
@@ -22,6 +23,7 @@ from mlx_tree_spec_amd import add_rms_norm_, add_rms_norm_qmm_, gate_up_silu, qu
 from mlx_tree_spec_amd import _lib
 from oracle import cpu
 from oracle import qmm4_oracle as O
+from route_cases import FOLD_CASES
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -55,21 +57,7 @@ def make_case(m, n, k, seed):
     return x, r, nw, w, s, b
 
 
-# (M, N, K, silu_mul): the form each takes.
-CASES = [
-    (1, 34816, 5120, True),    # decode gate+up, whole K (the decode MLP's first projection)
-    (2, 34816, 5120, True),
-    (4, 34816, 5120, True),
-    (1, 17408, 5120, False),   # whole K, plain
-    (3, 5120, 5120, False),    # small form
-    (4, 5120, 512, False),     # small form, one unit per block row
-    (2, 20480, 640, False),    # whole K, units of 5 super-steps
-    (2, 12288, 8192, False),   # K in 2 slices, the largest folded K (4 chunks per thread)
-    (1, 12288, 8192, True),    # gate+up in 2 K slices
-    (5, 5120, 5120, False),    # 5 rows: norm kernel + row-split (8-row fragments)
-    (4, 5120, 10240, False),   # K > 8192: norm kernel + projection
-    (16, 8192, 1024, True),    # 16 rows: norm kernel + two-pass gate+up
-]
+CASES = [c[:4] for c in FOLD_CASES]
 
 
 @pytest.mark.parametrize("m,n,k,silu_mul", CASES)

@@ -20,21 +20,65 @@ LIBDIR = os.path.join(ROOT, "mlx-tree-spec_amd", "mlx_tree_spec_amd")
 LIB = os.path.join(LIBDIR, "libqmm4.so")
 
 
-def test_planners_keep_kernel_invariants(tmp_path):
+@pytest.fixture(scope="module")
+def planner_exe(tmp_path_factory):
     if not os.path.exists(LIB):
         pytest.skip("libqmm4.so is not built (run __graft_entry__.build())")
     cxx = shutil.which("g++")
     if cxx is None:
         pytest.skip("g++ is not available")
-    exe = tmp_path / "plan_invariants"
+    exe = tmp_path_factory.mktemp("plans") / "plan_invariants"
     cmd = [cxx, "-std=c++17", "-O1", "-D__HIP_PLATFORM_AMD__", "-I/opt/rocm/include",
            "-I", os.path.join(ROOT, "include"), "-I", os.path.join(ROOT, "mlx-tree-spec_amd", "csrc"),
            os.path.join(ROOT, "tests", "plan_invariants.cpp"), "-L", LIBDIR, "-lqmm4",
            f"-Wl,-rpath,{LIBDIR}", "-o", str(exe)]
     build = subprocess.run(cmd, capture_output=True, text=True, timeout=300)
     assert build.returncode == 0, build.stderr[-4000:]
+    return str(exe)
+
+
+def query(exe, lines):
+    """The planners' forms for `lines` ("<planner> M N K cus" each), one output line per query."""
+    run = subprocess.run([exe, "query"], input="".join(ln + "\n" for ln in lines), capture_output=True,
+                         text=True, timeout=60)
+    assert run.returncode == 0, run.stderr
+    out = run.stdout.splitlines()
+    assert len(out) == len(lines)
+    return [dict(kv.split("=") for kv in o.split()) if "=" in o and not o.startswith("xreg") else o for o in out]
+
+
+def test_planners_keep_kernel_invariants(planner_exe):
+    exe = planner_exe
     run = subprocess.run([str(exe)], capture_output=True, text=True, timeout=300)
     assert run.returncode == 0, run.stdout[-4000:] + run.stderr[-2000:]
     assert "violations: 0" in run.stdout
     checked = int(run.stdout.split("plans checked:")[1].split(",")[0])
     assert checked > 10000, run.stdout
+
+
+def test_fold_cases_take_their_routes(planner_exe):
+    """Each shape of test_gpu_norm_fold.py reaches the form its label names on 256 CUs: the folded
+    row-split launch (4-row fragments, the regular form) with K whole or in 2 slices, or two
+    launches. The fold runs when dispatch_norm_qmm's condition holds: at most 4 rows and a row-split
+    plan (fused for the gate+up) that rowsplit_norm_ok accepts."""
+    from route_cases import CUS, FOLD_CASES
+
+    lines = [f"{'rowsplit_fused' if su else 'rowsplit'} {m} {n} {k} {CUS}" for m, n, k, su, _ in FOLD_CASES]
+    for (m, n, k, su, route), p in zip(FOLD_CASES, query(planner_exe, lines)):
+        folded = m <= 4 and isinstance(p, dict) and p["norm_ok"] == "1"
+        if route == "two launches":
+            assert not folded, (m, n, k, su, p)
+        else:
+            assert folded, (m, n, k, su, p)
+            assert p["MP"] == "4" and p["small"] == "0" and p["pair"] == "0" and p["own"] == "0"
+            assert route == f"fold KS={p['KS']}", (m, n, k, su, route, p)
+
+
+def test_gate_up_cases_take_their_routes(planner_exe):
+    """Each shape of test_gpu_mlp.py reaches its route on 256 CUs: the fused row-split launch when
+    rowsplit_plan(fused) accepts it (dispatch_gate_up_silu), else the two-pass path."""
+    from route_cases import CUS, GATE_UP_CASES
+
+    lines = [f"rowsplit_fused {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
+    for (m, k, n, route), p in zip(GATE_UP_CASES, query(planner_exe, lines)):
+        assert route == ("two-pass" if p == "none" else "fused"), (m, k, n, route, p)
