@@ -51,13 +51,13 @@ WORKLOADS = {
 # Mid-size M (a short prompt tail, more than 64 tree nodes): the model's up and down projections at
 # 65 to 2048 rows. name: (seed, rows, K, N, sigma)
 MID = {
-    "up": (6, (65, 128, 256, 512, 1024, 2048), 5120, 17408, 1.0),
-    "down": (7, (65, 128, 256, 512, 1024, 2048), 17408, 5120, 0.5),
+    "up": (6, (65, 80, 96, 112, 128, 256, 512, 1024, 2048), 5120, 17408, 1.0),
+    "down": (7, (65, 80, 96, 112, 128, 256, 512, 1024, 2048), 17408, 5120, 0.5),
 }
 # Every eligible linear of the target model (its seven (K, N) shapes) and its two vocabulary heads
 # (lm_head 5120 -> 248320, the drafter's 5120 -> 65984) at the decode (1, 4) and tree-verify
-# (16, 64) row counts. name: (seed, rows, K, N, sigma)
-MODEL = {f"{k}->{n}": (10 + i, (1, 4, 16, 64), k, n, 0.5 if k > 6144 else 1.0)
+# (16, 64, 96, 128) row counts. name: (seed, rows, K, N, sigma)
+MODEL = {f"{k}->{n}": (10 + i, (1, 4, 16, 64, 96, 128), k, n, 0.5 if k > 6144 else 1.0)
          for i, (k, n) in enumerate([(5120, 17408), (17408, 5120), (5120, 10240), (5120, 6144), (6144, 5120),
                                      (5120, 12288), (5120, 1024), (5120, 248320), (5120, 65984)])}
 # One GPU's share of an 8-way split by output columns (the way the path would shard): the decode

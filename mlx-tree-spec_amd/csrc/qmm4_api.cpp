@@ -333,6 +333,17 @@ int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, cons
 }
 
 // The kernel choice for y = x @ dequant(w)^T (arguments already checked, M and N > 0, api_mutex held).
+// Past 64 rows the row-phase kernel takes up to kRowPhaseMaxM rows over a small N (its weights are
+// dequantized once for all rows), and up to kRowPhaseMaxMNarrow when N is at most
+// kRowPhaseNarrowN (the GEMM then has too few 128 x 128 tiles). Measured against the GEMM (A/B,
+// interleaved rounds, the model's up and down projections): 65 / 80 / 96 / 112 rows 38.5 / 40.2 /
+// 44.2 / 47.4 us against 46.7 / 47.2 / 48.5 / 48.6 us (5120 -> 17408), 35.8 / 36.7 / 40.4 / 44.2
+// against 45.5 / 46.5 / 47.8 / 48.8 (17408 -> 5120); at 120-128 rows (one block per wave) 53-74
+// against 48-51 us, but 128 x 5120 -> 1024 17.3 against 47.6 us.
+constexpr int kRowPhaseMaxM = 112;
+constexpr int kRowPhaseMaxMNarrow = 128;
+constexpr int kRowPhaseNarrowN = 2048;
+
 int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* scales, const void* biases,
                  void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream, WorkspaceSource& ws) {
   const uint16_t* xb = static_cast<const uint16_t*>(x);
@@ -342,7 +353,28 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
   hipError_t e;
   int rc;
 
+  // The row-phase kernel on a plan (K split over the CUs when N is small, with its reduce kernel).
+  auto run_rowphase = [&](const RowPhasePlan& pplan) -> int {
+    uint32_t* pcnt = nullptr;
+    float* ppart = nullptr;
+    if (pplan.S > 1) {
+      int rc2 = ws.get(0, pplan.part_bytes, &pcnt, &ppart);
+      if (rc2) return rc2;
+    }
+    hipError_t e2 = launch_rowphase(pplan, xb, w, sb, bb, yb, ppart, (int)M, (int)N, (int)K, stream);
+    if (e2 != hipSuccess) return hip_error(e2, "row-phase kernel launch");
+    return QMM4_OK;
+  };
+
   if (M > 64) {
+    // 65-112 rows over a small N (a verify batch past 64 tree nodes, a short prompt tail): the
+    // row-phase kernel with 80-112-row x blocks, K split over the CUs. Its weights are dequantized
+    // once for all rows, where the GEMM's 128-row tiles pad these rows to 128.
+    if ((M <= kRowPhaseMaxM || (M <= kRowPhaseMaxMNarrow && N <= kRowPhaseNarrowN)) && aligned(scales, 16) &&
+        aligned(biases, 16) && K % 512 == 0) {
+      RowPhasePlan pplan;
+      if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) && !pplan.wide) return run_rowphase(pplan);
+    }
     GemmPlan gplan;
     gemm_plan((int)M, (int)N, (int)K, di->cus, ws.capacity(), sb, bb, &gplan);
     uint32_t* gcnt = nullptr;
@@ -390,17 +422,8 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
   if (M >= 5 && aligned(scales, 16) && aligned(biases, 16) && K % 512 == 0) {
     RowPhasePlan pplan;
     if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) &&
-        (pplan.wide || M >= 17 || 2 * pplan.blocks >= di->cus)) {
-      uint32_t* pcnt = nullptr;
-      float* ppart = nullptr;
-      if (pplan.S > 1) {
-        rc = ws.get(0, pplan.part_bytes, &pcnt, &ppart);
-        if (rc) return rc;
-      }
-      e = launch_rowphase(pplan, xb, w, sb, bb, yb, ppart, (int)M, (int)N, (int)K, stream);
-      if (e != hipSuccess) return hip_error(e, "row-phase kernel launch");
-      return QMM4_OK;
-    }
+        (pplan.wide || M >= 17 || 2 * pplan.blocks >= di->cus))
+      return run_rowphase(pplan);
   }
   if (M >= 5) {
     VerifyPlan vplan;

@@ -55,7 +55,7 @@ struct RowPhaseParams {
   int ranges;     // block ranges
 };
 
-template <int MB_, int V_, int BPW_, int W_>
+template <int MB_, int V_, int BPW_, int W_, int STG_ = 3>
 struct RpCfg {
   static constexpr int kRpWaves = W_;  // waves per workgroup
   static constexpr int kRpThreads = 64 * W_;
@@ -74,7 +74,9 @@ struct RpCfg {
   static constexpr int kWS = kWB + 16;
   static constexpr size_t kXBytes = (size_t)kXPieces * 16;
   static constexpr size_t kWinBytes = (size_t)RW * kWS;  // one array's window
-  static constexpr int kStages = 3;  // x stages: phase p in use, p + 1 staged, p + 2 being staged
+  // x stages: 3 = phase p in use, p + 1 staged, p + 2 being staged; 2 (80-row x, whose three
+  // stages would not fit beside the windows) = phase p in use, p + 1 being staged.
+  static constexpr int kStages = STG_;
   static constexpr size_t kYBytes = (size_t)MP * RW * 2;   // epilogue: bf16 tile of y
   static constexpr size_t kMain = kStages * kXBytes + 2 * kWinBytes;
   static constexpr size_t kLds = (kMain > kYBytes ? kMain : kYBytes);
@@ -82,6 +84,7 @@ struct RpCfg {
   static constexpr int kXL = (kXPieces + kRpThreads - 1) / kRpThreads;         // x loads per thread and phase
   static constexpr int kWL = (RW * (kWB / 16) + kRpThreads - 1) / kRpThreads;  // window loads per thread and array
   static_assert(V == 2 || V == 4, "phases of 2 or 4 super-steps");
+  static_assert(STG_ == 2 || STG_ == 3, "two or three x stages");
 };
 
 // Device-coherent 16-byte stores and loads (cache policy sc1: coherent across the XCDs' L2s).
@@ -278,9 +281,11 @@ void rowphase_kernel(RowPhaseParams P) {
     }
   };
 
-  // ---- prologue: x of phases pa and pa + 1, their weights, the scale window of phase pa ----
+  // ---- prologue: x of phase pa (and pa + 1 with three stages), the weights of phases pa and
+  // pa + 1, the scale window of phase pa ----
+  constexpr int kSt = C::kStages;
   stage_x(0, pa, np > 0);
-  stage_x(1, pa + 1, np > 1);
+  if constexpr (kSt == 3) stage_x(1, pa + 1, np > 1);
 #pragma unroll
   for (int v = 0; v < V; ++v) fetch_v(0, v, pa, np > 0);
 #pragma unroll
@@ -300,18 +305,19 @@ void rowphase_kernel(RowPhaseParams P) {
   }
   bool winbad = __syncthreads_or(store_window(wr)) != 0;
 
-  // Loads issued after the x of phase ph + 1 by the end of phase ph: the rest of phase ph - 1's
-  // weight refills, the x of phase ph + 2 and phase ph's refills.
-  constexpr int kAfter = 2 * BPW * V + C::kXL;
+  // Loads issued after the x of phase ph + 1 by the end of phase ph: with three stages the rest of
+  // phase ph - 1's weight refills, the x of phase ph + 2 and phase ph's refills; with two (x of
+  // phase ph + 1 issued at the start of phase ph) phase ph's refills.
+  constexpr int kAfter = kSt == 3 ? 2 * BPW * V + C::kXL : BPW * V;
   static_assert(kAfter < 64, "vector memory count range");
 
-  // ---- phase ph from register buffer J and x stage (ph - pa) % 3. Meanwhile phase ph + 2 is
-  // loaded: its x into stage (ph - pa + 2) % 3 (last read in phase ph - 1), its weights into
-  // buffer J as phase ph's pieces are used. A phase that starts a scale window restages the window
-  // first (after the previous phase's barrier). ----
+  // ---- phase ph from register buffer J and x stage (ph - pa) % kSt. Meanwhile the x of phase
+  // ph + kSt - 1 goes into stage (ph - pa + kSt - 1) % kSt (last read in phase ph - 1), and the
+  // weights of phase ph + 2 into buffer J as phase ph's pieces are used. A phase that starts a
+  // scale window restages the window first (after the previous phase's barrier). ----
   auto phase = [&](int ph, auto jc) __attribute__((always_inline)) {
     const int k = ph - pa;
-    const int st = k % 3, st2 = (k + 2) % 3, pw = ph % C::WP;
+    const int st = k % kSt, st2 = (k + kSt - 1) % kSt, pw = ph % C::WP;
     if (pw == 0 && k > 0) {
       if constexpr (kWinAhead) {
         // The window's registers were loaded during the previous phase, and every wave is past
@@ -331,9 +337,9 @@ void rowphase_kernel(RowPhaseParams P) {
     }
     const bool live2 = ph + 2 < pb;
     if (kWinAhead && pw == C::WP - 1 && ph + 1 < pb) load_window(ph + 1, wr);
-    stage_x(st2, ph + 2, live2);
+    stage_x(st2, ph + kSt - 1, ph + kSt - 1 < pb);
     compute(st, pw, jc, !winbad, ph + 2, live2);
-    // The x of phase ph + 1 (issued at the start of phase ph - 1) is in LDS; publish it. A bare
+    // The x of phase ph + 1 (issued at the start of phase ph + 2 - kSt) is in LDS; publish it. A bare
     // barrier: __syncthreads() would also wait for the x and weight loads of the phases ahead
     // (its fence covers the LDS writes of the DMA still in flight).
     asm volatile("s_waitcnt vmcnt(%0)" ::"n"(kAfter) : "memory");
@@ -461,30 +467,37 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
 
 }  // namespace
 
-// Kernel table: id -> (row blocks of x, super-steps per phase, blocks per wave, waves).
+// Kernel table: id -> (row blocks of x, super-steps per phase, blocks per wave, waves, x stages).
 #define QMM4_ROWPHASE_VARIANTS(X) \
-  X(0, 1, 2, 5, 8)                \
-  X(1, 2, 2, 5, 8)                \
-  X(2, 4, 2, 3, 8)                \
-  X(3, 1, 4, 2, 8)                \
-  X(4, 2, 4, 2, 8)                \
-  X(5, 4, 2, 2, 8)                \
-  X(6, 1, 4, 1, 8)                \
-  X(7, 2, 4, 1, 8)                \
-  X(8, 4, 2, 1, 8)                \
-  X(9, 1, 2, 3, 8)                \
-  X(10, 2, 2, 3, 8)               \
-  X(11, 1, 2, 4, 8)               \
-  X(12, 2, 2, 4, 8)
-constexpr int kRpVariants = 13;
+  X(0, 1, 2, 5, 8, 3)             \
+  X(1, 2, 2, 5, 8, 3)             \
+  X(2, 4, 2, 3, 8, 3)             \
+  X(3, 1, 4, 2, 8, 3)             \
+  X(4, 2, 4, 2, 8, 3)             \
+  X(5, 4, 2, 2, 8, 3)             \
+  X(6, 1, 4, 1, 8, 3)             \
+  X(7, 2, 4, 1, 8, 3)             \
+  X(8, 4, 2, 1, 8, 3)             \
+  X(9, 1, 2, 3, 8, 3)             \
+  X(10, 2, 2, 3, 8, 3)            \
+  X(11, 1, 2, 4, 8, 3)            \
+  X(12, 2, 2, 4, 8, 3)            \
+  X(13, 5, 2, 2, 8, 2)            \
+  X(14, 5, 2, 1, 8, 2)            \
+  X(15, 6, 2, 2, 8, 2)            \
+  X(16, 6, 2, 1, 8, 2)            \
+  X(17, 7, 2, 2, 8, 2)            \
+  X(18, 7, 2, 1, 8, 2)            \
+  X(19, 8, 2, 1, 8, 2)
+constexpr int kRpVariants = 20;
 
-#define QMM4_RPCFG(id, mb, v, bpw, w) typedef RpCfg<mb, v, bpw, w> RpCfg##id;
+#define QMM4_RPCFG(id, mb, v, bpw, w, stg) typedef RpCfg<mb, v, bpw, w, stg> RpCfg##id;
 QMM4_ROWPHASE_VARIANTS(QMM4_RPCFG)
 #undef QMM4_RPCFG
 
 static bool rowphase_geometry(int id, int* mb, int* v, int* bpw, size_t* lds, int* items, int* waves = nullptr) {
   switch (id) {
-#define QMM4_RPG(i, m, vv, b, w)                                                                     \
+#define QMM4_RPG(i, m, vv, b, w, stg)                                                                 \
   case i:                                                                                           \
     *mb = m; *v = vv; *bpw = b; *lds = RpCfg##i::kLds; *items = RpCfg##i::kItems;                    \
     if (waves) *waves = w;                                                                          \
@@ -497,7 +510,7 @@ static bool rowphase_geometry(int id, int* mb, int* v, int* bpw, size_t* lds, in
 
 static const void* rowphase_func(int id) {
   switch (id) {
-#define QMM4_RPF(i, m, vv, b, w) \
+#define QMM4_RPF(i, m, vv, b, w, stg) \
   case i: return reinterpret_cast<const void*>(&rowphase_kernel<RpCfg##i>);
     QMM4_ROWPHASE_VARIANTS(QMM4_RPF)
 #undef QMM4_RPF
@@ -508,8 +521,9 @@ static const void* rowphase_func(int id) {
 constexpr int kRpNarrowBpw = 2;  // blocks per wave when K is split
 
 bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
-  if (M < 1 || M > 64 || N % 16 != 0 || cus < 1) return false;
-  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : 4;
+  if (M < 1 || M > 128 || N % 16 != 0 || cus < 1) return false;
+  // Row blocks of x: 16, 32 or 64 rows, then 80 to 128 (variants with two x stages).
+  const int mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : (M + 15) / 16;
   const int NB = N / 16;
   const int ks = K / 128;
   // Row offsets of this kernel stay below 2 GiB (rows past the end are addressed at 2 GiB).
@@ -640,7 +654,7 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
   if (e != hipSuccess) return e;
   // K split: the reduce kernel's grid has one thread per f32x4 item of every range's tile.
   switch (plan.variant) {
-#define QMM4_RPL(i, m, vv, bb, w)                                                                            \
+#define QMM4_RPL(i, m, vv, bb, w, stg)                                                                       \
   case i:                                                                                                   \
     hipLaunchKernelGGL(rowphase_kernel<RpCfg##i>, dim3(plan.blocks), dim3(RpCfg##i::kRpThreads), plan.lds,   \
                        stream, P);                                                                          \

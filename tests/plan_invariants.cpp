@@ -110,7 +110,7 @@ void check_rowphase(int M, int N, int K, int cus) {
   ++g_checked;
   const char* f = "rowphase M=%d N=%d K=%d cus=%d";
 #define RP(cond) CHECK(cond, f, M, N, K, cus)
-  RP(M >= 1 && M <= 64);
+  RP(M >= 1 && M <= 128);
   RP(p.BW >= 1 && p.S >= 1 && p.NP >= 1 && p.ranges >= 1);
   RP((long long)p.ranges * p.BW * 16 >= N);
   RP(p.blocks == p.ranges * p.S);
@@ -218,7 +218,8 @@ int query() {
 
 int main(int argc, char** argv) {
   if (argc > 1 && std::string(argv[1]) == "query") return query();
-  const int Ms[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16, 17, 24, 32, 33, 48, 63, 64, 65, 128, 300, 1024, 4096};
+  const int Ms[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16, 17, 24, 32, 33, 48, 63, 64, 65, 80, 81, 96, 97, 112, 113,
+                    128, 300, 1024, 4096};
   const int Ns[] = {16, 32, 48, 256, 1024, 1040, 2048, 3072, 4096, 4112, 5120, 6144, 10240, 12288,
                     17408, 34816, 65984, 131072, 151936, 248320, 248336, 262144};
   const int Ks[] = {128, 256, 384, 512, 640, 1024, 2048, 2560, 4096, 5120, 6144, 8192, 12288, 17408, 20480};
@@ -232,7 +233,7 @@ int main(int argc, char** argv) {
             if (N % 32 == 0) check_rowsplit(M, N, K, cus, true);
             check_xreg(M, N, K, cus);
           }
-          if (M <= 64) check_rowphase(M, N, K, cus);
+          if (M <= 128) check_rowphase(M, N, K, cus);
           if (M <= 64) check_verify(M, N, K, cus);
           else check_gemm(M, N, K, cus);
         }

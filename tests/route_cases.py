@@ -11,6 +11,11 @@ Routes of the residual add + RMS norm folded into the projection (qmm4_add_rms_n
                   row; the slices' sums meet through the arrival counters);
   "two launches"  the norm kernel, then the projection on its n (more than 4 rows, K above the
                   folded 8192, or a row-split plan that cannot normalise while staging).
+Routes of 65-128 rows (qmm4_affine_bf16, dispatch_qmm):
+  "row-phase"  the row-phase kernel with 80-128-row x blocks and K split over the CUs: up to 112
+               rows, or 128 over at most 2048 columns, when K % 512 == 0 and N leaves the kernel's
+               plan narrow (a wide plan, N >= 32768 on 256 CUs, goes to the GEMM);
+  "gemm"       the GEMM (stream-K over 128 x 128 tiles at these rows).
 Routes of the gate+up SiLU·mul projection (qmm4_gate_up_silu_bf16):
   "fused"     one row-split launch with the epilogue fused;
   "two-pass"  the projection into the library's scratch, then the SiLU·mul pass (no fused
@@ -54,5 +59,21 @@ GATE_UP_CASES = [
     (3, 81920, 256, "two-pass"),
     (16, 20480, 1024, "two-pass"),
     (64, 5120, 1024, "two-pass"),  # row-phase underneath
-    (100, 512, 4096, "two-pass"),  # GEMM underneath
+    (100, 512, 4096, "two-pass"),  # row-phase underneath (112-row x blocks)
+    (136, 512, 4096, "two-pass"),  # GEMM underneath
+]
+
+# (M, N, K, route)
+MID_ROW_CASES = [
+    (65, 17408, 5120, "row-phase"),   # up projection, one row past 64 (80-row x blocks)
+    (65, 5120, 17408, "row-phase"),   # down projection
+    (80, 5120, 17408, "row-phase"),
+    (96, 8192, 2048, "row-phase"),    # 96-row blocks
+    (112, 5120, 6144, "row-phase"),   # 112-row blocks
+    (100, 2064, 1024, "row-phase"),   # one block per wave (few phases per workgroup)
+    (128, 1024, 5120, "row-phase"),   # 128-row blocks over a small N
+    (113, 5120, 17408, "gemm"),
+    (128, 17408, 5120, "gemm"),
+    (72, 34816, 5120, "gemm"),        # a wide row-phase plan
+    (96, 1024, 640, "gemm"),          # K % 512 != 0
 ]

@@ -22,6 +22,7 @@ import golden_io
 from mlx_tree_spec_amd import STATS, QuantizedLinear, dequantize, install, quantized_matmul
 from oracle import cpu
 from oracle import qmm4_oracle as O
+from route_cases import MID_ROW_CASES
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -216,7 +217,7 @@ def test_reference_prefill_kernel_shapes(m, k, n):
     check_qmm(host_bits(y).reshape(m, n), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}", (x, w, s, b))
 
 
-@pytest.mark.parametrize("m,k,n", [(65, 5120, 1024), (255, 128, 528), (256, 256, 256), (257, 1024, 784),
+@pytest.mark.parametrize("m,k,n", [(65, 1152, 1024), (255, 128, 528), (256, 256, 256), (257, 1024, 784),
                                    (1024, 5120, 1040), (4096, 1024, 512)])
 def test_qmm_gemm_shapes(m, k, n):
     x, w, s, b = O.make_inputs(m, k, n, seed=m + k)
@@ -230,8 +231,9 @@ def workload_ref(x, w, s, b):
 
 # Mid-size M with few output tiles takes the GEMM's stream-K form: 128 x 128 tiles x K units
 # spread over every resident workgroup, tiles split between workgroups added by a fix-up kernel in
-# K order. 65 rows of the down projection (40 tiles over 17408 of K), the up projection at 128 rows,
-# K = 1152 (units of two K steps: K % 512 != 0), N = 784 and M = 200 (partial column and row tiles).
+# K order. 65 rows over K = 17536 (40 tiles; K % 512 != 0 keeps 65 rows off the row-phase kernel,
+# units of two K steps), the up projection at 128 rows, K = 1152 and K = 640, N = 784 and M = 200
+# (partial column and row tiles).
 # Also where whole 256 x 256 tiles would fill under half the CUs: 256 and 320 rows of the up
 # projection (272 and 408 tiles of 128). Long K with fewer whole 256 x 256 tiles than CUs takes
 # stream-K over those: 512 and 1024 rows of the down projection (40 and 80 tiles), 384 x 12288 ->
@@ -239,8 +241,8 @@ def workload_ref(x, w, s, b):
 # tiles whose last round has fewer quarters than CUs run it as stream-K over the quarters: 1024 x
 # 5120 -> 17408 (272 tiles: 256 whole, 16 in quarters), 4096 x 1024 -> 1040 (80 tiles, a partial
 # column of tiles).
-@pytest.mark.parametrize("m,k,n", [(65, 17408, 5120), (128, 5120, 17408), (100, 1152, 4096), (200, 5120, 784),
-                                   (96, 512, 1024), (256, 5120, 17408), (320, 5120, 17408),
+@pytest.mark.parametrize("m,k,n", [(65, 17536, 5120), (128, 5120, 17408), (100, 1152, 4096), (200, 5120, 784),
+                                   (96, 640, 1024), (256, 5120, 17408), (320, 5120, 17408),
                                    (1024, 17408, 5120), (512, 17408, 5120), (384, 12288, 5120),
                                    (1000, 8192, 4112), (1024, 5120, 17408), (4096, 1024, 1040)])
 def test_gemm_stream_k_shapes(m, k, n):
@@ -329,7 +331,7 @@ MODEL_LINEARS = [(5120, 17408), (17408, 5120), (5120, 10240), (5120, 6144), (614
                  (5120, 1024)]
 
 
-@pytest.mark.parametrize("k,n,rows", [(k, n, (1, 4, 16, 48, 64, 128, 512)) for k, n in MODEL_LINEARS]
+@pytest.mark.parametrize("k,n,rows", [(k, n, (1, 4, 16, 48, 64, 96, 128, 512)) for k, n in MODEL_LINEARS]
                          + [(5120, 248320, (1, 4, 16, 32)), (5120, 65984, (1, 4, 6, 16, 32, 64))],
                          ids=lambda v: str(v) if not isinstance(v, tuple) else "rows")
 def test_model_linear_shapes(k, n, rows):
@@ -635,7 +637,8 @@ def test_rowphase_shapes(m, k, n):
     check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"row-phase {m}x{k}x{n}", (x, w, s, b))
 
 
-@pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48), (65984, 16), (131072, 32)])
+@pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48), (65984, 16), (131072, 32), (4096, 80), (2064, 112),
+                                 (1024, 128)])
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
     """One-hot rows of x on the row-phase path (wide and K-split): each output is one dequantized
@@ -661,13 +664,27 @@ def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
         assert not bad.any(), f"{int(bad.sum())} mismatches at k0={k0}, first {np.argwhere(bad)[:3].tolist()}"
 
 
+# 65-128 rows (a verify batch past 64 tree nodes, a short prompt tail): the row-phase kernel with
+# 80-128-row x blocks where its plan is narrow, else the GEMM (route_cases.MID_ROW_CASES; the routes
+# are checked against the planner in tests/test_plans.py).
+@pytest.mark.parametrize("m,n,k,route", MID_ROW_CASES)
+def test_mid_rows(m, n, k, route):
+    note(f"{route} {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, sigma=0.5 if k > 6144 else 1.0, seed=m * 13 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"{route} {m}x{k}x{n}", (x, w, s, b))
+    assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 # Scale windows of the row-phase kernel are 32 groups (2048 values of k) of every row. Odd windows
 # here hold scales that need the general form, even windows only fast-form scales, so a workgroup
 # whose phases cross windows switches form at each window: wide ranges of 10 and 12 phases over 3
 # and 2 windows (windows loaded a phase ahead), the K-split batched-verify shape (ranges of 5-6
 # phases, some across a window edge), and a wide 32-row shape whose variant stages each window at
 # its first phase (5 blocks per wave leave no registers for a window ahead).
-@pytest.mark.parametrize("m,k,n", [(8, 5120, 34848), (48, 3072, 33024), (64, 17408, 5120), (32, 5120, 65552)])
+@pytest.mark.parametrize("m,k,n", [(8, 5120, 34848), (48, 3072, 33024), (64, 17408, 5120), (32, 5120, 65552),
+                                   (96, 17408, 5120)])
 def test_rowphase_window_form_switches(m, k, n):
     note(f"row-phase window switches {m}x{k}x{n}")
     rng = np.random.default_rng(m * 7 + k)

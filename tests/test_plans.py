@@ -82,3 +82,16 @@ def test_gate_up_cases_take_their_routes(planner_exe):
     lines = [f"rowsplit_fused {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
     for (m, k, n, route), p in zip(GATE_UP_CASES, query(planner_exe, lines)):
         assert route == ("two-pass" if p == "none" else "fused"), (m, k, n, route, p)
+
+
+def test_mid_row_cases_take_their_routes(planner_exe):
+    """Each 65-128-row shape of test_gpu_parity.py reaches its route on 256 CUs: the row-phase
+    kernel when dispatch_qmm's condition holds (up to 112 rows, or 128 over at most 2048 columns;
+    K % 512 == 0; a narrow row-phase plan), else the GEMM."""
+    from route_cases import CUS, MID_ROW_CASES
+
+    lines = [f"rowphase {m} {n} {k} {CUS}" for m, n, k, _ in MID_ROW_CASES]
+    for (m, n, k, route), p in zip(MID_ROW_CASES, query(planner_exe, lines)):
+        rows_ok = m <= 112 or (m <= 128 and n <= 2048)
+        takes = rows_ok and k % 512 == 0 and isinstance(p, dict) and p["wide"] == "0"
+        assert route == ("row-phase" if takes else "gemm"), (m, n, k, route, p)

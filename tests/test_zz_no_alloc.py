@@ -156,7 +156,7 @@ PAIRS = [
     ((64, 5120, 17408), (24, 2048, 5120)),
     ((16, 512, 5120), (8, 256, 2048)),
     ((3, 256, 4096), (2, 64, 1024)),
-    ((96, 512, 1024), (80, 256, 512)),
+    ((96, 640, 1024), (80, 256, 512)),
     ((512, 5120, 17408), (128, 17408, 5120)),
     ((1024, 17408, 5120), (96, 512, 1024)),
 ]
