@@ -77,7 +77,9 @@ int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const
  * hipMalloc).
  *   - Calls no hipMalloc / hipFree / allocating routine. The first call on a device looks the array
  *     up, clears its counters on `hip_stream` and waits for that clear (that call must not be
- *     captured: QMM4_ERR_CAPTURE); later calls on that device may be captured.
+ *     captured: QMM4_ERR_CAPTURE); later calls on that device may be captured. The array takes
+ *     device memory from that first call on (HIP loads the code object holding it then), not
+ *     when the library is loaded.
  *   - A shape whose split-K buffers exceed the array returns QMM4_ERR_INVALID with the sizes.
  *   - Every call on one GPU shares that GPU's array: calls that overlap on one GPU (different
  *     streams, or threads without ordering between them) race. Order them on one stream.
