@@ -55,10 +55,13 @@ extern "C" {
  *   consecutive steps, or waves owning whole blocks, when N is as large as a vocabulary head) or a few K slices per workgroup,
  *   every unit in flight at once for small problems; row-phase for more than 16 rows, a large N,
  *   or fewer rows when its K split fills half the CUs; K-split verify or stream-K skinny
- *   otherwise), larger M the MFMA GEMM (whole 256 x 256 tiles, or stream-K over 128 x 128 tiles
- *   when whole tiles would leave many CUs idle, over 256 x 256 tiles when K is long too);
- *   the choice is a fixed function of the shape and the scale/bias alignment. Results are
- *   deterministic (bit-identical across calls and streams).
+ *   otherwise); 65-112 rows (128 over at most 2048 columns) the row-phase kernel with 80-128-row
+ *   x blocks when its plan is narrow; larger M the MFMA GEMM (whole 256 x 256 tiles, or stream-K
+ *   over 128 x 128 tiles when whole tiles would leave many CUs idle, over 256 x 256 tiles when K
+ *   is long too); the choice is a fixed function of the shape and the scale/bias alignment.
+ *   Results are deterministic (bit-identical across calls and streams). Other formats (2- or
+ *   8-bit codes, groups of 32 or 128) return QMM4_ERR_UNSUPPORTED: dequant4_affine_bf16 takes
+ *   them, and the package's quantized_matmul multiplies its output with a bf16 GEMM.
  */
 int qmm4_affine_bf16(const void* x, const uint32_t* w, const void* scales, const void* biases,
                      void* y, int64_t M, int64_t N, int64_t K, int group_size, int bits,
@@ -109,10 +112,16 @@ int qmm4_gate_up_silu_bf16(const void* x, const uint32_t* w, const void* scales,
                            int transpose, void* hip_stream);
 
 /*
- * out = dequant(w) as bf16 [N, K] — the bit-exact unpack + affine dequant.
- * Replaces mx.dequantize(w, scales, biases, group_size=64, bits=4) as used by the reference's
- * exact-reference definition (tests/test_units.py:108) and qmm_packed.py:200-201 / 635-636.
- *   Requires N >= 0, K % 64 == 0, group_size == 64, bits == 4, 16-byte aligned w and out.
+ * out = dequant(w) as bf16 [N, K] — the bit-exact unpack + affine dequant,
+ * out[n, k] = bf16_rne(fp32(s) * q + fp32(b)).
+ * Replaces mx.dequantize(w, scales, biases, group_size, bits) as used by the reference's
+ * exact-reference definition (tests/test_units.py:108) and qmm_packed.py:200-201 / 635-636, and
+ * by the general path the reference gives modules its packed kernels do not take
+ * (packed_linear.py:84-86).
+ *   bits 2, 4 or 8 (code k = (32 / bits) c + i in bits [bits i, bits i + bits) of word c of its
+ *   row, w uint32 [N, K * bits / 32]); group_size 32, 64 or 128 (scales and biases
+ *   [N, K / group_size]). Other bit widths return QMM4_ERR_UNSUPPORTED.
+ *   Requires N >= 0, K % group_size == 0, 16-byte aligned w and out.
  */
 int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
                          int64_t N, int64_t K, int group_size, int bits, void* hip_stream);

@@ -592,20 +592,25 @@ int qmm4_add_rms_norm_bf16(const void* x, const void* r, const void* weight, voi
 int dequant4_affine_bf16(const uint32_t* w, const void* scales, const void* biases, void* out,
                          int64_t N, int64_t K, int group_size, int bits, void* hip_stream) {
   qmm4::clear_error();
-  int rc = check_format(group_size, bits, 1);
-  if (rc) return rc;
-  if (N < 0 || K <= 0 || K % 64 != 0)
-    return set_error(QMM4_ERR_INVALID, "invalid shape N=%lld K=%lld (K must be a positive multiple of 64)",
-                (long long)N, (long long)K);
+  // MLX's affine formats whose codes fill whole uint32 words: 2, 4 or 8 bits in groups of 32, 64
+  // or 128 (mx.dequantize's parameters).
+  if (bits != 2 && bits != 4 && bits != 8)
+    return set_error(QMM4_ERR_UNSUPPORTED, "bits=%d: dequantize supports 2-, 4- and 8-bit codes", bits);
+  if (group_size != 32 && group_size != 64 && group_size != 128)
+    return set_error(QMM4_ERR_UNSUPPORTED, "group_size=%d: dequantize supports groups of 32, 64 and 128", group_size);
+  if (N < 0 || K <= 0 || K % group_size != 0)
+    return set_error(QMM4_ERR_INVALID, "invalid shape N=%lld K=%lld (K must be a positive multiple of group_size=%d)",
+                     (long long)N, (long long)K, group_size);
+  if (N > (1LL << 30) || K > (1LL << 30))
+    return set_error(QMM4_ERR_INVALID, "shape N=%lld K=%lld exceeds 2^30", (long long)N, (long long)K);
   if (N == 0) return QMM4_OK;
   if (!w || !scales || !biases || !out) return set_error(QMM4_ERR_INVALID, "null pointer argument");
   if (!aligned(w, 16) || !aligned(out, 16))
     return set_error(QMM4_ERR_INVALID, "w and out must be 16-byte aligned");
   if (!aligned(scales, 2) || !aligned(biases, 2))
     return set_error(QMM4_ERR_INVALID, "scales and biases must be 2-byte aligned");
-  hipError_t e = qmm4::launch_dequant(w, static_cast<const uint16_t*>(scales),
-                                      static_cast<const uint16_t*>(biases),
-                                      static_cast<uint16_t*>(out), N, K,
+  hipError_t e = qmm4::launch_dequant(w, static_cast<const uint16_t*>(scales), static_cast<const uint16_t*>(biases),
+                                      static_cast<uint16_t*>(out), N, K, group_size, bits,
                                       static_cast<hipStream_t>(hip_stream));
   if (e != hipSuccess) return hip_error(e, "dequant kernel launch");
   return QMM4_OK;

@@ -151,8 +151,9 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
                        const uint16_t* b, uint16_t* y, float* part, int M, int N, int K, int cus,
                        hipStream_t stream);
 
-// Bit-exact dequantization to bf16 [N, K].
-hipError_t launch_dequant(const uint32_t* w, const uint16_t* s, const uint16_t* b,
-                          uint16_t* out, int64_t N, int64_t K, hipStream_t stream);
+// Bit-exact dequantization to bf16 [N, K]: 4-bit codes in groups of 64 (the packed kernels'
+// format), or 2-, 4- or 8-bit codes in groups of 32, 64 or 128 (K % group_size == 0).
+hipError_t launch_dequant(const uint32_t* w, const uint16_t* s, const uint16_t* b, uint16_t* out, int64_t N,
+                          int64_t K, int group_size, int bits, hipStream_t stream);
 
 }  // namespace qmm4

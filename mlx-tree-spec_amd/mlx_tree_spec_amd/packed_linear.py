@@ -36,7 +36,8 @@ STATS: dict[str, int] = defaultdict(int)
 
 
 class QuantizedLinear(torch.nn.Module):
-    """y = x @ dequant(weight).T (+ bias) for MLX-format affine 4-bit weights."""
+    """y = x @ dequant(weight).T (+ bias) for MLX-format affine weights: 4-bit codes in groups of
+    64 on the packed kernels; 2-, 4- and 8-bit codes in groups of 32, 64 or 128 on the general path."""
 
     def __init__(self, input_dims: int, output_dims: int, bias: bool = False, group_size: int = 64,
                  bits: int = 4, mode: str = "affine", device=None):
@@ -176,8 +177,9 @@ def _call(self: QuantizedLinear, x: torch.Tensor) -> torch.Tensor:
     rows = math.prod(sh[:-1])
     if "_fast" not in self.__dict__ and not eligible(self):
         # packed_linear._call (84-86): a module the packed path does not take runs the general op
-        # (here quantized_matmul's dequantize + GEMM form for 4-bit shapes the kernels refuse; other
-        # formats raise NotImplementedError).
+        # (here quantized_matmul's exact dequantize + bf16 GEMM form: 4-bit shapes the kernels
+        # refuse, and 2-, 4- or 8-bit codes in groups of 32, 64 or 128; other widths raise
+        # NotImplementedError).
         STATS["fallback"] += 1
         y = quantized_matmul(x, self.weight, self.scales, self.biases, transpose=True,
                              group_size=self.group_size, bits=self.bits, mode=self.mode)

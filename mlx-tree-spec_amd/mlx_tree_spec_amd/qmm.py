@@ -10,8 +10,8 @@ Mirrors the reference's calls:
          packed_linear.py:72-80), kept for interoperability: the gfx950 kernels read MLX's own
          [N, K/8] layout, so weights in the reference's packed layout are converted back once.
 
-Tensors: x bfloat16 (..., K) on a HIP device; w int32 or uint32 [N, K/8] (the bits are used as
-is); scales and biases bfloat16 [N, K/64]. Output bfloat16 (..., N), allocated here, written
+Tensors: x bfloat16 (..., K) on a HIP device; w int32 or uint32 [N, K * bits / 32] (the bits are
+used as is); scales and biases bfloat16 [N, K / group_size]. Output bfloat16 (..., N), allocated here, written
 asynchronously on the current stream of x's device.
 """
 
@@ -24,13 +24,30 @@ from . import _lib
 _W_DTYPES = (torch.int32, torch.uint32)
 
 
-def _check_format(group_size: int, bits: int, transpose: bool = True, mode: str = "affine") -> None:
+# MLX affine formats whose codes fill whole uint32 words (code k = (32 / bits) c + i in bits
+# [bits i, bits i + bits) of word c): dequantize takes them all, and so does quantized_matmul,
+# whose packed kernels implement 4 bits in groups of 64 (other formats: dequantize, then a bf16
+# GEMM, as the reference leaves them to MLX's own op, packed_linear.py:84-86). 3-, 5- and 6-bit
+# codes, which MLX packs across word boundaries, are not supported.
+GENERAL_BITS = (2, 4, 8)
+GENERAL_GROUP_SIZES = (32, 64, 128)
+
+
+def _check_format(group_size: int, bits: int, transpose: bool = True, mode: str = "affine",
+                  general: bool = False) -> None:
     if mode != "affine":
         raise NotImplementedError(f"mode={mode!r}: only 'affine' quantization is supported")
-    if bits != 4:
-        raise NotImplementedError(f"bits={bits}: only 4-bit codes are supported")
-    if group_size != 64:
-        raise NotImplementedError(f"group_size={group_size}: only group_size=64 is supported")
+    if general:
+        if bits not in GENERAL_BITS:
+            raise NotImplementedError(f"bits={bits}: only {', '.join(map(str, GENERAL_BITS))}-bit codes are supported")
+        if group_size not in GENERAL_GROUP_SIZES:
+            raise NotImplementedError(f"group_size={group_size}: only group sizes "
+                                      f"{', '.join(map(str, GENERAL_GROUP_SIZES))} are supported")
+    else:
+        if bits != 4:
+            raise NotImplementedError(f"bits={bits}: only 4-bit codes are supported")
+        if group_size != 64:
+            raise NotImplementedError(f"group_size={group_size}: only group_size=64 is supported")
     if not transpose:
         raise NotImplementedError("transpose=False: only y = x @ dequant(w).T is supported")
 
@@ -80,12 +97,13 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
                      mode: str = "affine") -> torch.Tensor:
     """y = x @ dequant(w).T in bf16 with fp32 accumulation (HIP kernels; no CPU path).
 
-    Shapes the packed kernels take (K % 128 == 0, N % 16 == 0) run them. Other shapes of the
-    format (K % 64 == 0, any N) are what the reference leaves to MLX's own op (packed_linear.py:
-    56-57, 84-86): the weights are dequantized exactly by the HIP kernel and multiplied by a bf16
-    GEMM with fp32 accumulation on the same stream.
+    Shapes the packed kernels take (4-bit codes in groups of 64, K % 128 == 0, N % 16 == 0) run
+    them. Other shapes (K % 64 == 0, any N) and formats (2-, 4- or 8-bit codes in groups of 32, 64
+    or 128) are what the reference leaves to MLX's own op (packed_linear.py:56-57, 84-86): the
+    weights are dequantized exactly by the HIP kernel and multiplied by a bf16 GEMM with fp32
+    accumulation on the same stream.
     """
-    _check_format(group_size, bits, transpose, mode)
+    _check_format(group_size, bits, transpose, mode, general=True)
     if x.dtype != torch.bfloat16:
         raise ValueError(f"[quantized_matmul] x must be bfloat16, got {x.dtype}")
     if x.dim() < 1:
@@ -97,7 +115,7 @@ def quantized_matmul(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, bia
     dev = _check_device("quantized_matmul", x, w, scales, biases)
     x2 = aligned_contiguous(x.reshape(-1, k))
     m = x2.shape[0]
-    if k % 128 or n % 16:
+    if k % 128 or n % 16 or bits != 4 or group_size != 64:
         wd = dequantize(w, scales, biases, group_size, bits)
         return torch.nn.functional.linear(x2, wd).reshape(*x.shape[:-1], n)
     w = aligned_contiguous(w)
@@ -149,8 +167,9 @@ def gate_up_silu(x: torch.Tensor, w: torch.Tensor, scales: torch.Tensor, biases:
 
 def dequantize(w: torch.Tensor, scales: torch.Tensor, biases: torch.Tensor, group_size: int = 64,
                bits: int = 4, mode: str = "affine") -> torch.Tensor:
-    """bf16 [N, K] with w_deq = bf16_rne(fp32(s) * q + fp32(b)), bit-exact (HIP kernel)."""
-    _check_format(group_size, bits, True, mode)
+    """bf16 [N, K] with w_deq = bf16_rne(fp32(s) * q + fp32(b)), bit-exact (HIP kernel); 2-, 4- or
+    8-bit codes in groups of 32, 64 or 128 (mx.dequantize's parameters)."""
+    _check_format(group_size, bits, True, mode, general=True)
     n, k = _check_weights(w, scales, biases, None, group_size, bits, "dequantize")
     dev = _check_device("dequantize", w, scales, biases)
     w = aligned_contiguous(w)

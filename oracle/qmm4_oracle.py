@@ -6,6 +6,7 @@ its HIP library is missing.
 
 Restates, in numpy, the reference's arithmetic for the path:
   * codes:    q[n, 8c+i] = (w[n, c] >> 4i) & 0xF                 src/mlx_tree_spec/qmm_packed.py:115, 200-201
+              (2- and 8-bit codes, the general path's other whole-word formats, in the same order)
   * groups:   g = k // 64, scales/biases bf16 [N, K/64]          qmm_packed.py:454, 630
   * dequant:  bf16_rne(fp32(s) * q + fp32(b))                    qmm_packed.py:200-201, 348-349, 635-636
   * matmul:   y = fp32(x) @ fp32(dequant(w)).T, bf16 out         tests/test_units.py:108 ("exact")
@@ -45,37 +46,44 @@ def bf16_bits_to_f32(u) -> np.ndarray:
 
 
 # ----------------------------------------------------------------------------- format
-def unpack_codes(w) -> np.ndarray:
-    """uint32 [N, K/8] -> uint8 codes [N, K]; code k = 8c + i sits in bits [4i, 4i+4) of word c."""
+def unpack_codes(w, bits: int = BITS) -> np.ndarray:
+    """uint32 [N, K * bits / 32] -> uint8 codes [N, K]; code k = (32 / bits) c + i sits in bits
+    [bits i, bits i + bits) of word c (4 bits: qmm_packed.py:115, 200-201; 2 and 8 bits, the formats
+    MLX packs into whole words, the same little-endian order)."""
+    assert bits in (2, 4, 8)
+    per = 32 // bits
     w = np.asarray(w, dtype=np.uint32)
     n, kw = w.shape
-    shifts = (4 * np.arange(8, dtype=np.uint32))[None, None, :]
-    q = (w[:, :, None] >> shifts) & np.uint32(0xF)
-    return q.reshape(n, kw * 8).astype(np.uint8)
+    shifts = (bits * np.arange(per, dtype=np.uint32))[None, None, :]
+    q = (w[:, :, None] >> shifts) & np.uint32((1 << bits) - 1)
+    return q.reshape(n, kw * per).astype(np.uint8)
 
 
-def pack_codes(q) -> np.ndarray:
-    """uint8 codes [N, K] (values 0..15) -> uint32 [N, K/8]; inverse of unpack_codes."""
+def pack_codes(q, bits: int = BITS) -> np.ndarray:
+    """uint8 codes [N, K] (values below 2^bits) -> uint32 [N, K * bits / 32]; inverse of unpack_codes."""
+    assert bits in (2, 4, 8)
+    per = 32 // bits
     q = np.asarray(q, dtype=np.uint32)
     n, k = q.shape
-    assert k % 8 == 0
-    q = q.reshape(n, k // 8, 8)
-    w = np.zeros((n, k // 8), dtype=np.uint32)
-    for i in range(8):
-        w |= (q[:, :, i] & 0xF) << np.uint32(4 * i)
+    assert k % per == 0
+    q = q.reshape(n, k // per, per)
+    w = np.zeros((n, k // per), dtype=np.uint32)
+    for i in range(per):
+        w |= (q[:, :, i] & np.uint32((1 << bits) - 1)) << np.uint32(bits * i)
     return w
 
 
 def dequantize(w, scales, biases, group_size: int = GROUP_SIZE, bits: int = BITS) -> np.ndarray:
     """bf16 bits [N, K] of bf16_rne(fp32_rne(s * q + b)), s * q + b taken exactly (FMA semantics).
 
-    s * q has at most 12 significant bits, so it is exact in float64 (and float64 has the
-    exponent range to hold it even where it would overflow fp32 while s * q + b does not). The
-    float64 sum is then rounded to fp32: rounding a sum of two values with <= 24-bit significands
-    first to float64 and then to fp32 equals rounding it once to fp32 (53 >= 2*24 + 2).
+    s * q has at most 16 significant bits (8-bit codes), so it is exact in float64 (and float64
+    has the exponent range to hold it even where it would overflow fp32 while s * q + b does not).
+    The float64 sum is then rounded to fp32: rounding a sum of two values with <= 24-bit
+    significands first to float64 and then to fp32 equals rounding it once to fp32 (53 >= 2*24 + 2).
+    bits 2, 4 or 8; group_size 32, 64 or 128.
     """
-    assert bits == 4 and group_size == 64
-    q = unpack_codes(w).astype(np.float64)
+    assert bits in (2, 4, 8) and group_size in (32, 64, 128)
+    q = unpack_codes(w, bits).astype(np.float64)
     n, k = q.shape
     s = np.repeat(bf16_bits_to_f32(scales).astype(np.float64), group_size, axis=1)
     b = np.repeat(bf16_bits_to_f32(biases).astype(np.float64), group_size, axis=1)

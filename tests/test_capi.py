@@ -178,7 +178,12 @@ def test_dequant_rejects():
     p = 0x10000
     assert lib.dequant4_affine_bf16(p, p, p, p, 8, 96, 64, 4, None) == _lib.QMM4_ERR_INVALID
     assert "K" in _lib.last_error()
-    assert lib.dequant4_affine_bf16(p, p, p, p, 8, 128, 64, 2, None) == _lib.QMM4_ERR_UNSUPPORTED
+    for gs, bits in ((64, 3), (64, 5), (64, 6), (64, 16), (16, 4), (256, 8)):
+        assert lib.dequant4_affine_bf16(p, p, p, p, 8, 256, gs, bits, None) == _lib.QMM4_ERR_UNSUPPORTED
+        assert (f"bits={bits}" if bits not in (2, 4, 8) else f"group_size={gs}") in _lib.last_error()
+    # K must be whole groups of the format's group size.
+    assert lib.dequant4_affine_bf16(p, p, p, p, 8, 96, 32 * 2, 8, None) == _lib.QMM4_ERR_INVALID
+    assert lib.dequant4_affine_bf16(p, p, p, p, 8, 64, 128, 2, None) == _lib.QMM4_ERR_INVALID
     assert lib.dequant4_affine_bf16(0, p, p, p, 8, 128, 64, 4, None) == _lib.QMM4_ERR_INVALID
     assert lib.dequant4_affine_bf16(p + 4, p, p, p, 8, 128, 64, 4, None) == _lib.QMM4_ERR_INVALID
     assert lib.dequant4_affine_bf16(0, 0, 0, 0, 0, 128, 64, 4, None) == _lib.QMM4_OK

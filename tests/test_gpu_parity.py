@@ -371,6 +371,59 @@ def test_quantized_linear_ineligible_module_falls_back():
     assert O.max_rel(got, ref) <= O.MAX_REL_TOL
 
 
+def general_inputs(m, k, n, bits, group_size, seed):
+    """Inputs in one of the general path's formats: codes uniform over 0 .. 2^bits - 1, scales
+    |N(0, 1)| * 0.004 + 1e-4 and biases centring the codes, as make_inputs draws the 4-bit ones."""
+    rng = np.random.default_rng(seed)
+    x = O.f32_to_bf16_bits(rng.standard_normal((m, k)).astype(np.float32))
+    w = rng.integers(0, 2**32, size=(n, k * bits // 32), dtype=np.uint32)
+    s = O.f32_to_bf16_bits((np.abs(rng.standard_normal((n, k // group_size))) * 0.004 + 1e-4).astype(np.float32))
+    b = O.f32_to_bf16_bits((-(2.0 ** (bits - 1)) * O.bf16_bits_to_f32(s)
+                            + rng.standard_normal((n, k // group_size)) * 1e-3).astype(np.float32))
+    return x, w, s, b
+
+
+GENERAL_FORMATS = [(2, 32), (2, 64), (2, 128), (4, 32), (4, 128), (8, 32), (8, 64), (8, 128)]
+
+
+@pytest.mark.parametrize("bits,group_size", GENERAL_FORMATS)
+def test_dequant_general_formats(bits, group_size):
+    """2-, 4- and 8-bit codes in groups of 32, 64 or 128 (mx.dequantize's parameters; the general
+    path of modules the packed kernels do not take, packed_linear.py:84-86): bit-exact against the
+    oracle, whose decode and dequant are pinned against row bit strings and exact rationals."""
+    note(f"dequant {bits}-bit group {group_size}")
+    for n, k in ((96, 1024), (33, 4096)):
+        _, w, s, b = general_inputs(1, k, n, bits, group_size, seed=bits * 1000 + group_size + k)
+        got = host_bits(dequantize(u32_dev(w), bf16_dev(s), bf16_dev(b), group_size=group_size, bits=bits))
+        assert np.array_equal(got, O.dequantize(w, s, b, group_size, bits)), (bits, group_size, n, k)
+
+
+@pytest.mark.parametrize("bits,group_size", GENERAL_FORMATS)
+def test_qmm_general_formats(bits, group_size):
+    """quantized_matmul in the general formats (exact HIP dequantize, then a bf16 GEMM with fp32
+    accumulation) against the fp32-accumulated oracle, at decode, verify and prefill rows."""
+    for m, k, n in ((1, 1024, 256), (16, 2048, 320), (80, 512, 1024), (300, 1024, 512)):
+        note(f"qmm {bits}-bit group {group_size} {m}x{k}x{n}")
+        x, w, s, b = general_inputs(m, k, n, bits, group_size, seed=m + k + n + bits)
+        y = host_bits(quantized_matmul(bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b),
+                                       group_size=group_size, bits=bits))
+        check_qmm(y, O.quantized_matmul_exact(x, w, s, b, group_size, bits), f"{bits}-bit g{group_size} {m}x{k}x{n}")
+
+
+def test_quantized_linear_other_formats_fall_back():
+    """An 8-bit (or 2-bit, or group-128) module is not eligible for the packed kernels and runs the
+    general path, as the reference's _call sends it to MLX's op (packed_linear.py:84-86)."""
+    from mlx_tree_spec_amd import STATS, QuantizedLinear, eligible
+    for bits, group_size in ((8, 64), (2, 32), (4, 128)):
+        x, w, s, b = general_inputs(5, 512, 192, bits, group_size, seed=bits + group_size)
+        mod = QuantizedLinear.from_quantized(u32_dev(w), bf16_dev(s), bf16_dev(b), group_size=group_size, bits=bits)
+        assert not eligible(mod) and mod.input_dims == 512
+        before = STATS["fallback"]
+        y = host_bits(mod(bf16_dev(x)))
+        assert STATS["fallback"] == before + 1
+        check_qmm(y, O.quantized_matmul_exact(x, w, s, b, group_size, bits), f"{bits}-bit g{group_size} module")
+
+
 def test_workload_prefill_sampled_rows():
     """The 4096 x 5120 -> 17408 prefill GEMM on the GPU; 256 sampled rows against the oracle."""
     x, w, s, b = O.config_inputs(4)

@@ -23,12 +23,29 @@ def test_no_cpu_path():
         dequantize(w, s, b)
 
 
-@pytest.mark.parametrize("kw,exc", [(dict(bits=8), NotImplementedError), (dict(group_size=32), NotImplementedError),
+@pytest.mark.parametrize("kw,exc", [(dict(bits=3), NotImplementedError), (dict(bits=6), NotImplementedError),
+                                    (dict(group_size=16), NotImplementedError),
                                     (dict(transpose=False), NotImplementedError), (dict(mode="mxfp4"), NotImplementedError)])
 def test_format_errors(kw, exc):
     x, w, s, b = tensors()
     with pytest.raises(exc):
         quantized_matmul(x, w, s, b, **kw)
+
+
+@pytest.mark.parametrize("bits,group_size", [(8, 64), (2, 32), (4, 128)])
+def test_general_formats_are_accepted(bits, group_size):
+    """2-, 4- and 8-bit codes in groups of 32, 64 or 128 pass the format checks (the general path:
+    HIP dequantize, then a bf16 GEMM); on CPU tensors the call then stops at the device check."""
+    n, k = 64, 256
+    x = torch.zeros((2, k), dtype=torch.bfloat16)
+    w = torch.zeros((n, k * bits // 32), dtype=torch.int32)
+    s = torch.zeros((n, k // group_size), dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="HIP device"):
+        quantized_matmul(x, w, s, s, group_size=group_size, bits=bits)
+    with pytest.raises(ValueError, match="HIP device"):
+        dequantize(w, s, s, group_size=group_size, bits=bits)
+    with pytest.raises(ValueError, match="does not match"):  # weights of another width
+        quantized_matmul(x, w, s, s, group_size=group_size, bits=8 if bits == 4 else 4)
 
 
 def test_shape_and_dtype_errors():

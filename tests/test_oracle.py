@@ -2,11 +2,15 @@
 
 How each oracle function is pinned:
   unpack_codes / pack_codes  bytes-view decode of qmm_packed.py:115-116 (independent of shifts);
-                             brute-force fixture; round trip
+                             brute-force fixture; round trip; for the general path's 2- and 8-bit
+                             words, the rows' little-endian bit strings cut into fields (8 bits:
+                             the bytes themselves); parity unpinned beyond that shared formula
+                             (MLX's own packing of other widths is not in the reference)
   f32_to_bf16_bits           torch's own fp32 -> bf16 conversion (round to nearest even)
   dequantize                 exact-rational brute-force fixture (incl. 257 double-rounding
                              entries); closed forms s=1,b=0 -> q; q=0 -> b; s=0 -> b;
-                             group mapping with distinct per-group scales
+                             group mapping with distinct per-group scales; 2/4/8-bit codes in
+                             groups of 32/64/128 against the exact-rational dequant
   quantized_matmul(_exact)   brute-force fixture (exact rational sums); one-hot x picks single
                              dequantized weights; integer codes with s=1, b=0 against integer
                              arithmetic; linearity and power-of-two scaling
@@ -49,6 +53,62 @@ def test_unpack_codes_matches_bytes_view():
 def test_unpack_codes_single_word():
     w = np.array([[0x76543210, 0xFEDCBA98]], dtype=np.uint32)
     assert O.unpack_codes(w).tolist() == [list(range(16))]
+
+
+def row_bit_string_codes(w, bits):
+    """Codes of each row read from the row's whole little-endian bit string (one Python integer per
+    row): code k is bits [bits k, bits k + bits) of it. Independent of per-word shifts."""
+    w = np.ascontiguousarray(w, dtype="<u4")
+    out = []
+    for row in w:
+        v = int.from_bytes(row.tobytes(), "little")
+        out.append([(v >> (bits * k)) & ((1 << bits) - 1) for k in range(row.size * 32 // bits)])
+    return np.array(out, dtype=np.uint8)
+
+
+@pytest.mark.parametrize("bits", [2, 4, 8])
+def test_unpack_codes_general_bits_against_row_bit_string(bits):
+    """The general path's whole-word formats: code k = (32 / bits) c + i in bits [bits i, bits i +
+    bits) of word c is the row's little-endian bit string cut into bits-wide fields (4 bits: the
+    byte view above, qmm_packed.py:115-116)."""
+    rng = np.random.default_rng(bits)
+    w = rng.integers(0, 2**32, size=(5, 12), dtype=np.uint32)
+    q = O.unpack_codes(w, bits)
+    assert np.array_equal(q, row_bit_string_codes(w, bits))
+    assert np.array_equal(O.pack_codes(q, bits), w)
+    if bits == 8:  # the codes are the words' little-endian bytes
+        assert np.array_equal(q, np.ascontiguousarray(w, dtype="<u4").view(np.uint8).reshape(5, -1))
+    # A planted mistake: fields taken from the top of each word down.
+    per = 32 // bits
+    rev = q.reshape(5, -1, per)[:, :, ::-1].reshape(5, -1)
+    assert not np.array_equal(rev, row_bit_string_codes(w, bits))
+
+
+@pytest.mark.parametrize("bits,group_size", [(2, 32), (2, 128), (8, 32), (8, 64), (8, 128), (4, 32), (4, 128)])
+def test_dequantize_general_formats_exact_rational(bits, group_size):
+    """dequantize for the general path's formats against the exact-rational dequant of
+    tests/golden/make_golden.py (bf16_rne(fp32_rne(s * q + b)) computed with Fractions), codes
+    read from the row bit strings, each group's own scale and bias (distinct per group)."""
+    import sys
+    import os
+    sys.path.insert(0, os.path.join(os.path.dirname(os.path.abspath(__file__)), "golden"))
+    import make_golden as G
+
+    rng = np.random.default_rng(100 * bits + group_size)
+    n, k = 3, 256
+    w = rng.integers(0, 2**32, size=(n, k * bits // 32), dtype=np.uint32)
+    sf = (np.abs(rng.standard_normal((n, k // group_size))) * 0.01 + 1e-3).astype(np.float32)
+    s = O.f32_to_bf16_bits(sf)
+    b = O.f32_to_bf16_bits((-(2 ** (bits - 1)) * O.bf16_bits_to_f32(s)
+                            + rng.standard_normal((n, k // group_size)).astype(np.float32) * 1e-3).astype(np.float32))
+    got = O.dequantize(w, s, b, group_size, bits)
+    q = row_bit_string_codes(w, bits)
+    want = np.array([[G.dequant_one(int(s[i, j // group_size]), int(b[i, j // group_size]), int(q[i, j]))
+                      for j in range(k)] for i in range(n)], dtype=np.uint16)
+    assert np.array_equal(got, want)
+    # A planted mistake: the neighbouring group's scale.
+    s2 = np.roll(s, 1, axis=1)
+    assert not np.array_equal(O.dequantize(w, s2, b, group_size, bits), want)
 
 
 def test_bf16_rounding_matches_torch():
