@@ -290,15 +290,19 @@ void rowphase_kernel(RowPhaseParams P) {
   for (int v = 0; v < V; ++v) fetch_v(0, v, pa, np > 0);
 #pragma unroll
   for (int v = 0; v < V; ++v) fetch_v(1, v, pa + 1, np > 1);
-  // Windows are aligned to absolute phases (WP-phase boundaries of K), so every 16-byte piece of
-  // a window is 16-byte aligned. The window's loads return after the x loads above (the vector
-  // memory count is in order), so its stores also find both x stages written.
+  // The window's loads return after the x loads above (the vector memory count is in order), so
+  // its stores also find both x stages written.
   // Later windows are loaded into registers one phase ahead where the registers allow
   // (accumulators, two weight buffers and the window within 150 of the 256 VGPRs); otherwise a
   // window is loaded and stored at its first phase.
   constexpr bool kWinAhead = 4 * BPW * MB + 8 * BPW * V + 8 * C::kWL <= 150;
   u32x4 wr[2][C::kWL];
-  load_window(pa - pa % C::WP, wr);
+  // Windows start at the workgroup's first phase, rounded down so the window's first group is a
+  // multiple of 8 (every 16-byte piece then 16-byte aligned): a K slice reads the scale bytes of
+  // its own phases, not those of every WP-phase block of K it straddles (c2's 12 slices of 68
+  // phases used to read two windows each where one covers them).
+  const int wbase = pa - pa % (4 / V);
+  load_window(wbase, wr);
   if (tid == 0) {
     s_bad[0] = 0;
     s_bad[1] = 0;
@@ -317,12 +321,12 @@ void rowphase_kernel(RowPhaseParams P) {
   // scale window restages the window first (after the previous phase's barrier). ----
   auto phase = [&](int ph, auto jc) __attribute__((always_inline)) {
     const int k = ph - pa;
-    const int st = k % kSt, st2 = (k + kSt - 1) % kSt, pw = ph % C::WP;
+    const int st = k % kSt, st2 = (k + kSt - 1) % kSt, pw = (ph - wbase) % C::WP;
     if (pw == 0 && k > 0) {
       if constexpr (kWinAhead) {
         // The window's registers were loaded during the previous phase, and every wave is past
         // its last read of the old window (the previous phase's barrier).
-        const int wpar = (ph / C::WP) & 1;
+        const int wpar = ((ph - wbase) / C::WP) & 1;
         if (store_window(wr)) s_bad[wpar] = 1;
         if (tid == 0) s_bad[wpar ^ 1] = 0;  // last read one window ago
         asm volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
