@@ -12,6 +12,10 @@
 // activations and [BN][64 + 8] for the dequantized weights (147 KB at 256 x 256); the 144-byte
 // row pitch keeps the 16-byte fragment reads free of bank conflicts.
 //
+// Whole 256 x 256 tiles with 8-group scale blocks (K % 512 == 0, the prefill projections) run
+// gemm_ws_kernel instead: the same tiles and MFMA order, with four extra waves doing all loads,
+// dequantization and LDS stores while the eight MFMA waves only read fragments and multiply.
+//
 // Pipeline: the raw inputs of a K step (activation chunks, packed codes) are loaded into registers
 // two steps ahead of their use (four in the stream-K launches), through buffer resources (rows past M and columns past N read as
 // zero); scales and biases come 8 groups per 16-byte load when K % 512 == 0. While the MFMAs of
@@ -505,6 +509,214 @@ hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Whole 256 x 256 tiles with K % 512 == 0, waves split by role: waves 0-7 (two per SIMD, the 2 x 4
+// wave grid and MFMA order of gemm_kernel, so the same bits) only read fragments and run MFMAs;
+// waves 8-11 (one per SIMD) only load, dequantize and store the next K step into the other LDS
+// stage. A SIMD overlaps one wave's MFMAs with another wave's VALU far better than MFMAs and VALU
+// interleaved inside one wave: a dequantization wave beside an MFMA wave ran in the time of the
+// dequantization alone, where waves mixing both ran in ~0.8 of the sum of the two. 12 waves share
+// the SIMDs' 512 registers per lane: at most 168 per wave (146 used).
+// Producer thread pt (0-255): activation chunk pt % 8 of rows pt / 8 + 32 j (j < 8) and the 8 code
+// words (one group, 64 k) of column pt per K step, two steps ahead in registers; the column's scale
+// and bias come 8 groups per 16-byte load.
+constexpr int kWsProd = 4;                                  // producer waves
+constexpr int kWsThreads = 64 * (kWaves + kWsProd);
+constexpr int kWsD = 2;                                     // K steps of raw inputs in registers
+__global__ __launch_bounds__(kWsThreads) __attribute__((amdgpu_waves_per_eu(3)))
+void gemm_ws_kernel(GemmParams P) {
+  using C = GemmCfg<256, 256>;
+  constexpr int BM = 256, BN = 256, I = C::I, J = C::J, LDC = C::LDC;
+  extern __shared__ __attribute__((aligned(16))) uint16_t smem[];
+  uint16_t* As = smem;
+  uint16_t* Bs = smem + 2 * BM * LDK;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int nk = P.K / BK;  // a multiple of 8
+  const int G = gridDim.x;
+  int bid = blockIdx.x;
+  if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
+  int m0, n0;
+  {
+    const int id = P.tile0 + bid;
+    const int per_group = kGroupM * P.tiles_n;
+    const int group = id / per_group;
+    const int first_m = group * kGroupM;
+    const int gm = min(kGroupM, P.tiles_m - first_m);
+    const int in_group = id - group * per_group;
+    m0 = (first_m + in_group % gm) * kTile;
+    n0 = (in_group / gm) * kTile;
+  }
+  const int lrow = lane & 31;
+  const int lk = (lane >> 5) * 8;
+  f32x16 acc[I][J];
+#pragma unroll
+  for (int i = 0; i < I; ++i)
+#pragma unroll
+    for (int j = 0; j < J; ++j)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+
+  if (wave < kWaves) {
+    const int wm = wave / kWavesN, wn = wave % kWavesN;
+    __syncthreads();  // step 0 is in stage 0
+    auto step = [&](int st) __attribute__((always_inline)) {
+      const uint16_t* as = As + st * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
+      const uint16_t* bs = Bs + st * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
+      bf16x8 Af[2][I], Bf[2][J];
+      auto frags = [&](int ks, int sl) __attribute__((always_inline)) {
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+          Af[sl][i] = as_bf16x8(*reinterpret_cast<const u32x4*>(as + i * 32 * LDK + ks * 16));
+#pragma unroll
+        for (int j = 0; j < J; ++j)
+          Bf[sl][j] = as_bf16x8(*reinterpret_cast<const u32x4*>(bs + j * 32 * LDK + ks * 16));
+      };
+      frags(0, 0);
+#pragma unroll
+      for (int ks = 0; ks < BK / 16; ++ks) {
+        if (ks + 1 < BK / 16) frags(ks + 1, (ks + 1) & 1);
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+#pragma unroll
+          for (int j = 0; j < J; ++j) acc[i][j] = Mfma<32>::mma(Af[ks & 1][i], Bf[ks & 1][j], acc[i][j]);
+      }
+      __syncthreads();
+    };
+    for (int kt = 0; kt < nk; kt += 2) {
+      step(0);
+      step(1);
+    }
+    // The tile as bf16 into LDS (every wave is past the last step's reads: the loop's last barrier).
+    uint16_t* Cs = smem;
+#pragma unroll
+    for (int i = 0; i < I; ++i)
+#pragma unroll
+      for (int j = 0; j < J; ++j) {
+        const int n = wn * C::WN + j * 32 + lrow;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int m = wm * C::WM + i * 32 + Mfma<32>::row(lane, r);
+          Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
+        }
+      }
+  } else {
+    const int pt = tid - 64 * kWaves;
+    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint32_t*>(P.w), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 1)), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.s), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
+    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
+    const int a_kc = pt & 7, a_r0 = pt >> 3;
+    constexpr int kAJ = 8;                    // activation chunks per thread and step (rows a_r0 + 32 j)
+    const int xrowp = 32 * P.K * 2;
+    const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
+    const uint32_t col = (uint32_t)(n0 + pt);
+    const uint32_t woff = col * (uint32_t)(P.K >> 1);
+    const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
+    struct RawW { u32x4 a[kAJ]; u32x4 w[2]; };
+    RawW raw[kWsD];
+    auto load = [&](int kt, RawW& R) __attribute__((always_inline)) {
+      const int k = kt < nk ? kt : nk - 1;
+#pragma unroll
+      for (int j = 0; j < kAJ; ++j) R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrowp, 0);
+#pragma unroll
+      for (int v = 0; v < 2; ++v) R.w[v] = __builtin_amdgcn_raw_buffer_load_b128(rw, woff + v * 16, k * 32, 0);
+    };
+    u32x4 scur, bcur, snext = {0u, 0u, 0u, 0u}, bnext = snext;
+    auto load_sb8 = [&](int kt, u32x4& s8, u32x4& b8) __attribute__((always_inline)) {
+      const int k = kt < nk ? kt : 0;
+      s8 = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 2, 0);
+      b8 = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 2, 0);
+    };
+    auto pick_c = [&](const u32x4& v, auto gc) __attribute__((always_inline)) {
+      constexpr int Gi = decltype(gc)::value;
+      const uint32_t w = Gi / 2 == 0 ? v.x : Gi / 2 == 1 ? v.y : Gi / 2 == 2 ? v.z : v.w;
+      return (Gi & 1) ? (w >> 16) : (w & 0xFFFFu);
+    };
+    auto put = [&](const RawW& R, int st, uint32_t sbits, uint32_t bbits) __attribute__((always_inline)) {
+      uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
+#pragma unroll
+      for (int j = 0; j < kAJ; ++j) *reinterpret_cast<u32x4*>(as + 32 * j * LDK) = R.a[j];
+      uint16_t* bs = Bs + st * BN * LDK + pt * LDK;
+      const float sf = bf16_to_f32(sbits), bf = bf16_to_f32(bbits);
+      if (fast_scale_ok(sbits)) {
+        const float s24 = sf * 16777216.0f, s20 = sf * 1048576.0f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word_fast(R.w[j >> 2][j & 3], s24, s20, bf);
+      } else {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
+      }
+    };
+    // Prologue: steps 0 .. D - 1 in registers, step 0 into stage 0, then step D in flight.
+#pragma unroll
+    for (int i = 0; i < kWsD; ++i) load(i, raw[i]);
+    load_sb8(0, scur, bcur);
+    put(raw[0], 0, pick_c(scur, std::integral_constant<int, 0>{}), pick_c(bcur, std::integral_constant<int, 0>{}));
+    load(kWsD, raw[0]);
+    __syncthreads();
+    // Iteration kt (MMA waves on stage kt % 2): step kt + 1 into stage (kt + 1) % 2, then step
+    // kt + 1 + D loaded into its registers. Unrolled by 8 so each step's group is static.
+    auto it = [&](int kt, auto uc) __attribute__((always_inline)) {
+      constexpr int U = decltype(uc)::value;
+      constexpr int G1 = (U + 1) & 7;
+      RawW& R = raw[(U + 1) % kWsD];
+      if (kt + 1 < nk) {
+        const uint32_t sb = pick_c(U < 7 ? scur : snext, std::integral_constant<int, G1>{});
+        const uint32_t bb = pick_c(U < 7 ? bcur : bnext, std::integral_constant<int, G1>{});
+        put(R, (U + 1) & 1, sb, bb);
+      }
+      load(kt + 1 + kWsD, R);
+      if constexpr (U == 1) load_sb8(kt + 7, snext, bnext);  // the next block, first used at step kt + 7
+      __syncthreads();
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    for (int kt = 0; kt < nk; kt += 8) {
+      it(kt, std::integral_constant<int, 0>{});
+      it(kt + 1, std::integral_constant<int, 1>{});
+      it(kt + 2, std::integral_constant<int, 2>{});
+      it(kt + 3, std::integral_constant<int, 3>{});
+      it(kt + 4, std::integral_constant<int, 4>{});
+      it(kt + 5, std::integral_constant<int, 5>{});
+      it(kt + 6, std::integral_constant<int, 6>{});
+      it(kt + 7, std::integral_constant<int, 7>{});
+      scur = snext;
+      bcur = bnext;
+    }
+  }
+  __syncthreads();
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+  uint16_t* Cs = smem;
+  constexpr int kChunksPerRow = BN / 8;
+#pragma unroll 4
+  for (int c = tid; c < BM * kChunksPerRow; c += kWsThreads) {
+    const int r = c / kChunksPerRow, ch = c % kChunksPerRow;
+    const int gn = n0 + ch * 8;
+    if (gn < P.N) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
+      __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)(m0 + r) * (uint32_t)P.N + (uint32_t)gn) * 2u, 0, 0);
+    }
+  }
+}
+
+hipError_t launch_ws(const GemmParams& P, int blocks, hipStream_t stream) {
+  constexpr size_t smem = GemmCfg<256, 256>::kSmem;
+  static bool attr_set = false;  // the attribute is per function; setting it twice is harmless
+  if (!attr_set) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&gemm_ws_kernel),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem);
+    if (e != hipSuccess) return e;
+    attr_set = true;
+  }
+  hipLaunchKernelGGL(gemm_ws_kernel, dim3(blocks), dim3(kWsThreads), smem, stream, P);
+  return hipGetLastError();
+}
+
 template <int BM, int BN>
 hipError_t launch_sk_reduce(const GemmParams& P, int G, hipStream_t stream) {
   const long long items = (long long)P.sk_tiles * GemmCfg<BM, BN>::kPartF4;
@@ -668,7 +880,7 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
   if (main_tiles > 0) {
     P.tile0 = 0;
     P.quarter = 0;
-    hipError_t e = sb8 ? launch_tiles<256, 256, true>(P, main_tiles, stream)
+    hipError_t e = sb8 ? launch_ws(P, main_tiles, stream)
                        : launch_tiles<256, 256, false>(P, main_tiles, stream);
     if (e != hipSuccess) return e;
   }
