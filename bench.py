@@ -60,6 +60,15 @@ MID = {
 MODEL = {f"{k}->{n}": (10 + i, (1, 4, 16, 64, 96, 128), k, n, 0.5 if k > 6144 else 1.0)
          for i, (k, n) in enumerate([(5120, 17408), (17408, 5120), (5120, 10240), (5120, 6144), (6144, 5120),
                                      (5120, 12288), (5120, 1024), (5120, 248320), (5120, 65984)])}
+# Shapes that reach the two fallback kernels (no shape of the target model does): the K-split verify
+# kernel (5-16 rows over a small N with K too long for the row-phase split to fill half the CUs)
+# and the stream-K skinny kernel (up to 4 rows where the row-split planner refuses: tiny K and N).
+# name: (seed, rows, K, N, sigma)
+FALLBACK = {
+    "verify 17408->256": (20, (12, 16), 17408, 256, 0.5),
+    "skinny 128->16": (21, (1, 4), 128, 16, 1.0),
+    "skinny 256->48": (22, (3,), 256, 48, 1.0),
+}
 # One GPU's share of an 8-way split by output columns (the way the path would shard): the decode
 # gate+up and the vocab head at N / 8 columns. name: (seed, rows, K, N / 8, sigma)
 SHARD8 = {
@@ -116,7 +125,8 @@ class Workload:
         self.name, self.rows, self.k, self.n = name, rows, k, n
         x, w, s, b = synthetic_inputs(max(rows), k, n, sigma=sigma, seed=idx)
         wbytes = n * k // 2 + 4 * n * (k // 64)
-        self.copies = max(2, int(np.ceil(ROTATE_BYTES / wbytes)))
+        # (at most 4096 copies: the fallback shapes' weights are a few kilobytes)
+        self.copies = max(2, min(4096, int(np.ceil(ROTATE_BYTES / wbytes))))
         t = lambda a, dt: torch.from_numpy(np.ascontiguousarray(a).view(dt)).to(dev)
         w0, s0, b0 = t(w, np.int32), t(s, np.int16), t(b, np.int16)
         self.w = [w0] + [w0.clone() for _ in range(self.copies - 1)]
@@ -328,7 +338,8 @@ def measure_layer_tail(torch, dev, rows_list=(4, 64), n_layers: int = 2, samples
 def measure_rows(torch, lib, dev, samples: int, table: dict, floors: dict | None = None) -> dict:
     """Per-call medians (HIP events per launch, rotating weight copies) of each shape of `table` at
     its row counts, with HBM and bf16-MFMA fractions of peak: the up and down projections at 65 to
-    2048 rows (MID), every linear and head of the model at decode and verify rows (MODEL)."""
+    2048 rows (MID), every linear and head of the model at decode and verify rows (MODEL), the
+    shapes that reach the fallback kernels (FALLBACK)."""
     out = {}
     for name, spec in table.items():
         wl = Workload(name, torch, lib, dev, spec=spec)
@@ -646,6 +657,10 @@ def main() -> int:
     if not args.no_model:
         log("[bench] the model's linears and heads at decode and verify rows")
         model = measure_rows(torch, lib, dev, args.samples, MODEL, floors)
+    fallback = {}
+    if not args.no_model:
+        log("[bench] the fallback kernels (shapes no model linear has)")
+        fallback = measure_rows(torch, lib, dev, args.samples, FALLBACK, floors)
     log("[bench] one GPU's share of an 8-way column split")
     shard8 = measure_shard8(torch, lib, dev, args.samples)
     log("[bench] fused ops either side of the projection")
@@ -717,6 +732,7 @@ def main() -> int:
         "workloads": out_workloads,
         "mid_m": mid,
         "model_linears": model,
+        "fallback_kernels": fallback,
         "shard8": shard8,
         "fused": fused,
     }
