@@ -12,9 +12,10 @@
 // activations and [BN][64 + 8] for the dequantized weights (147 KB at 256 x 256); the 144-byte
 // row pitch keeps the 16-byte fragment reads free of bank conflicts.
 //
-// Whole 256 x 256 tiles with 8-group scale blocks (K % 512 == 0, the prefill projections) run
-// gemm_ws_kernel instead: the same tiles and MFMA order, with four extra waves doing all loads,
-// dequantization and LDS stores while the eight MFMA waves only read fragments and multiply.
+// 256 x 256 tiles with 8-group scale blocks (K % 512 == 0, the prefill projections), whole or in
+// stream-K segments, run gemm_ws_kernel instead: the same tiles, MFMA order and partial slots,
+// with four extra waves doing all loads, dequantization and LDS stores while the eight MFMA waves
+// only read fragments and multiply.
 //
 // Pipeline: the raw inputs of a K step (activation chunks, packed codes) are loaded into registers
 // two steps ahead of their use (four in the stream-K launches), through buffer resources (rows past M and columns past N read as
@@ -509,7 +510,7 @@ hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// Whole 256 x 256 tiles with K % 512 == 0, waves split by role: waves 0-7 (two per SIMD, the 2 x 4
+// 256 x 256 tiles with K % 512 == 0 (whole, or stream-K segments), waves split by role: waves 0-7 (two per SIMD, the 2 x 4
 // wave grid and MFMA order of gemm_kernel, so the same bits) only read fragments and run MFMAs;
 // waves 8-11 (one per SIMD) only load, dequantize and store the next K step into the other LDS
 // stage. A SIMD overlaps one wave's MFMAs with another wave's VALU far better than MFMAs and VALU
@@ -532,34 +533,78 @@ void gemm_ws_kernel(GemmParams P) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int nk = P.K / BK;  // a multiple of 8
+  const bool mma = wave < kWaves;
+  const int wm = wave / kWavesN, wn = wave % kWavesN;  // MFMA waves: the 2 x 4 grid of gemm_kernel
+  const int nk = P.K / BK;                              // a multiple of 8
   const int G = gridDim.x;
   int bid = blockIdx.x;
-  if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);
-  int m0, n0;
-  {
-    const int id = P.tile0 + bid;
+  if ((G & 7) == 0) bid = (bid & 7) * (G >> 3) + (bid >> 3);  // gemm_kernel's XCD-contiguous remap
+  auto tile_origin = [&](int id, int* m0, int* n0) __attribute__((always_inline)) {
     const int per_group = kGroupM * P.tiles_n;
     const int group = id / per_group;
     const int first_m = group * kGroupM;
     const int gm = min(kGroupM, P.tiles_m - first_m);
     const int in_group = id - group * per_group;
-    m0 = (first_m + in_group % gm) * kTile;
-    n0 = (in_group / gm) * kTile;
-  }
+    *m0 = (first_m + in_group % gm) * kTile;
+    *n0 = (in_group / gm) * kTile;
+  };
   const int lrow = lane & 31;
   const int lk = (lane >> 5) * 8;
-  f32x16 acc[I][J];
-#pragma unroll
-  for (int i = 0; i < I; ++i)
-#pragma unroll
-    for (int j = 0; j < J; ++j)
-#pragma unroll
-      for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+  const int pt = tid - 64 * kWaves;  // producer thread
+  const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint32_t*>(P.w), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 1)), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.s), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
+  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+  // The output tile's 16-byte row chunks from LDS, by all 12 waves; rows past M fall outside y's
+  // buffer resource, columns past N are skipped.
+  auto store_chunks = [&](int m0, int n0) __attribute__((always_inline)) {
+    const uint16_t* Cs = smem;
+    constexpr int kChunksPerRow = BN / 8;
+#pragma unroll 4
+    for (int c = tid; c < BM * kChunksPerRow; c += kWsThreads) {
+      const int r = c / kChunksPerRow, ch = c % kChunksPerRow;
+      const int gn = n0 + ch * 8;
+      if (gn < P.N) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
+        __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)(m0 + r) * (uint32_t)P.N + (uint32_t)gn) * 2u, 0, 0);
+      }
+    }
+  };
+  // The workgroup's tile segments: the whole K of tile P.tile0 + bid, or its stream-K range of units
+  // (gemm_kernel's bookkeeping: the same ranges, segments and partial slots, so
+  // gemm_sk_reduce_kernel adds the same bits). f(m0, n0, kb, ke, first) per segment.
+  auto for_segments = [&](auto f) __attribute__((always_inline)) {
+    if (!P.sk) {
+      int m0, n0;
+      tile_origin(P.tile0 + bid, &m0, &n0);
+      f(m0, n0, 0, nk, true);
+      return;
+    }
+    const long long u0 = sk_start(bid, P.U, G), u1 = sk_start(bid + 1, P.U, G);
+    for (long long u = u0; u < u1;) {
+      const int t = (int)(u / P.upt);
+      const long long tb = (long long)t * P.upt;
+      const long long e = u1 < tb + P.upt ? u1 : tb + P.upt;
+      int m0, n0;
+      tile_origin(t, &m0, &n0);
+      f(m0, n0, (int)(u - tb) * P.ups, (int)(e - tb) * P.ups, u == u0);
+      u = e;
+    }
+  };
+  // Every segment passes the same barriers in both roles: one after the producers' prologue, one
+  // per K step, one between the bf16 tile's LDS writes and its stores (whole tiles), one at the end
+  // (the next segment's prologue reuses the LDS stages and the output tile).
 
-  if (wave < kWaves) {
-    const int wm = wave / kWavesN, wn = wave % kWavesN;
-    __syncthreads();  // step 0 is in stage 0
+  if (mma) {
+    const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
+        P.part, 0, rsrc_bytes((unsigned long long)G * 2 * C::kPartF4 * 16), kBufferRsrcWord3);
+    f32x16 acc[I][J];
     auto step = [&](int st) __attribute__((always_inline)) {
       const uint16_t* as = As + st * BM * LDK + (wm * C::WM + lrow) * LDK + lk;
       const uint16_t* bs = Bs + st * BN * LDK + (wn * C::WN + lrow) * LDK + lk;
@@ -583,44 +628,77 @@ void gemm_ws_kernel(GemmParams P) {
       }
       __syncthreads();
     };
-    for (int kt = 0; kt < nk; kt += 2) {
-      step(0);
-      step(1);
-    }
-    // The tile as bf16 into LDS (every wave is past the last step's reads: the loop's last barrier).
-    uint16_t* Cs = smem;
+    for_segments([&](int m0, int n0, int kb, int ke, bool first) __attribute__((always_inline)) {
 #pragma unroll
-    for (int i = 0; i < I; ++i)
+      for (int i = 0; i < I; ++i)
 #pragma unroll
-      for (int j = 0; j < J; ++j) {
-        const int n = wn * C::WN + j * 32 + lrow;
+        for (int j = 0; j < J; ++j)
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int m = wm * C::WM + i * 32 + Mfma<32>::row(lane, r);
-          Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
-        }
+          for (int r = 0; r < 16; ++r) acc[i][j][r] = 0.0f;
+      __syncthreads();  // step kb is in stage 0
+      for (int kt = kb; kt < ke; kt += 2) {
+        step(0);
+        step(1);
       }
-  } else {
-    const int pt = tid - 64 * kWaves;
-    const __amdgpu_buffer_rsrc_t rx = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(P.x), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint32_t*>(P.w), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 1)), kBufferRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rs = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(P.s), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
-    const __amdgpu_buffer_rsrc_t rb = __builtin_amdgcn_make_buffer_rsrc(
-        const_cast<uint16_t*>(P.b), 0, rsrc_bytes((unsigned long long)P.N * (P.K >> 6) * 2), kBufferRsrcWord3);
-    const int a_kc = pt & 7, a_r0 = pt >> 3;
-    constexpr int kAJ = 8;                    // activation chunks per thread and step (rows a_r0 + 32 j)
-    const int xrowp = 32 * P.K * 2;
+      if (kb == 0 && ke == nk) {
+        // The tile as bf16 into LDS (every wave is past the last step's reads).
+        uint16_t* Cs = smem;
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+#pragma unroll
+          for (int j = 0; j < J; ++j) {
+            const int n = wn * C::WN + j * 32 + lrow;
+#pragma unroll
+            for (int r = 0; r < 16; ++r) {
+              const int m = wm * C::WM + i * 32 + Mfma<32>::row(lane, r);
+              Cs[m * LDC + n] = (uint16_t)(pack_bf16x2(acc[i][j][r], 0.0f) & 0xFFFFu);
+            }
+          }
+        __syncthreads();
+        store_chunks(m0, n0);
+      } else {
+        // A part of the tile: its fp32 sums to this workgroup's slot (0: its first segment, 1: its
+        // last), item-major per lane, as gemm_kernel stores them.
+        const uint32_t slot = (uint32_t)bid * 2u + (first ? 0u : 1u);
+#pragma unroll
+        for (int i = 0; i < I; ++i)
+#pragma unroll
+          for (int j = 0; j < J; ++j)
+#pragma unroll
+            for (int rq = 0; rq < 4; ++rq) {
+              const uint32_t item = (uint32_t)((((wave * I + i) * J + j) * 4 + rq) * 64 + lane);
+              const f32x4 v = {acc[i][j][4 * rq], acc[i][j][4 * rq + 1], acc[i][j][4 * rq + 2], acc[i][j][4 * rq + 3]};
+              __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, v), rp,
+                                                     (slot * (uint32_t)C::kPartF4 + item) * 16u, 0, 0);
+            }
+      }
+      __syncthreads();
+    });
+    return;
+  }
+
+  // Producers.
+  const int a_kc = pt & 7, a_r0 = pt >> 3;
+  constexpr int kAJ = 8;  // activation chunks per thread and step (rows a_r0 + 32 j)
+  const int xrowp = 32 * P.K * 2;
+  struct RawW {
+    u32x4 a[kAJ];
+    u32x4 w[2];
+  };
+  auto pick_c = [&](const u32x4& v, auto gc) __attribute__((always_inline)) {
+    constexpr int Gi = decltype(gc)::value;
+    const uint32_t w = Gi / 2 == 0 ? v.x : Gi / 2 == 1 ? v.y : Gi / 2 == 2 ? v.z : v.w;
+    return (Gi & 1) ? (w >> 16) : (w & 0xFFFFu);
+  };
+  for_segments([&](int m0, int n0, int kb, int ke, bool) __attribute__((always_inline)) {
     const uint32_t xoff = (uint32_t)(m0 + a_r0) * (uint32_t)P.K * 2u + (uint32_t)a_kc * 16u;
     const uint32_t col = (uint32_t)(n0 + pt);
     const uint32_t woff = col * (uint32_t)(P.K >> 1);
     const uint32_t soff = col * (uint32_t)(P.K >> 6) * 2u;
-    struct RawW { u32x4 a[kAJ]; u32x4 w[2]; };
     RawW raw[kWsD];
+    // Steps past the segment's last are clamped to it (loaded into registers that are not stored).
     auto load = [&](int kt, RawW& R) __attribute__((always_inline)) {
-      const int k = kt < nk ? kt : nk - 1;
+      const int k = kt < ke ? kt : ke - 1;
 #pragma unroll
       for (int j = 0; j < kAJ; ++j) R.a[j] = __builtin_amdgcn_raw_buffer_load_b128(rx, xoff, k * BK * 2 + j * xrowp, 0);
 #pragma unroll
@@ -628,14 +706,9 @@ void gemm_ws_kernel(GemmParams P) {
     };
     u32x4 scur, bcur, snext = {0u, 0u, 0u, 0u}, bnext = snext;
     auto load_sb8 = [&](int kt, u32x4& s8, u32x4& b8) __attribute__((always_inline)) {
-      const int k = kt < nk ? kt : 0;
+      const int k = kt < ke ? kt : kb;
       s8 = __builtin_amdgcn_raw_buffer_load_b128(rs, soff, k * 2, 0);
       b8 = __builtin_amdgcn_raw_buffer_load_b128(rb, soff, k * 2, 0);
-    };
-    auto pick_c = [&](const u32x4& v, auto gc) __attribute__((always_inline)) {
-      constexpr int Gi = decltype(gc)::value;
-      const uint32_t w = Gi / 2 == 0 ? v.x : Gi / 2 == 1 ? v.y : Gi / 2 == 2 ? v.z : v.w;
-      return (Gi & 1) ? (w >> 16) : (w & 0xFFFFu);
     };
     auto put = [&](const RawW& R, int st, uint32_t sbits, uint32_t bbits) __attribute__((always_inline)) {
       uint16_t* as = As + st * BM * LDK + a_r0 * LDK + a_kc * 8;
@@ -652,20 +725,20 @@ void gemm_ws_kernel(GemmParams P) {
         for (int j = 0; j < 8; ++j) *reinterpret_cast<u32x4*>(bs + j * 8) = dequant_word(R.w[j >> 2][j & 3], sf, sf * 0.0625f, bf);
       }
     };
-    // Prologue: steps 0 .. D - 1 in registers, step 0 into stage 0, then step D in flight.
+    // Prologue: steps kb .. kb + D - 1 in registers, step kb into stage 0, then step kb + D in flight.
 #pragma unroll
-    for (int i = 0; i < kWsD; ++i) load(i, raw[i]);
-    load_sb8(0, scur, bcur);
+    for (int i = 0; i < kWsD; ++i) load(kb + i, raw[i]);
+    load_sb8(kb, scur, bcur);
     put(raw[0], 0, pick_c(scur, std::integral_constant<int, 0>{}), pick_c(bcur, std::integral_constant<int, 0>{}));
-    load(kWsD, raw[0]);
+    load(kb + kWsD, raw[0]);
     __syncthreads();
-    // Iteration kt (MMA waves on stage kt % 2): step kt + 1 into stage (kt + 1) % 2, then step
-    // kt + 1 + D loaded into its registers. Unrolled by 8 so each step's group is static.
+    // Iteration kt (the MFMA waves on stage (kt - kb) % 2): step kt + 1 into the other stage, then
+    // step kt + 1 + D loaded into its registers. Unrolled by 8, so each step's group is static.
     auto it = [&](int kt, auto uc) __attribute__((always_inline)) {
       constexpr int U = decltype(uc)::value;
       constexpr int G1 = (U + 1) & 7;
       RawW& R = raw[(U + 1) % kWsD];
-      if (kt + 1 < nk) {
+      if (kt + 1 < ke) {
         const uint32_t sb = pick_c(U < 7 ? scur : snext, std::integral_constant<int, G1>{});
         const uint32_t bb = pick_c(U < 7 ? bcur : bnext, std::integral_constant<int, G1>{});
         put(R, (U + 1) & 1, sb, bb);
@@ -675,7 +748,7 @@ void gemm_ws_kernel(GemmParams P) {
       __syncthreads();
       __builtin_amdgcn_sched_barrier(0);
     };
-    for (int kt = 0; kt < nk; kt += 8) {
+    for (int kt = kb; kt < ke; kt += 8) {
       it(kt, std::integral_constant<int, 0>{});
       it(kt + 1, std::integral_constant<int, 1>{});
       it(kt + 2, std::integral_constant<int, 2>{});
@@ -687,21 +760,12 @@ void gemm_ws_kernel(GemmParams P) {
       scur = snext;
       bcur = bnext;
     }
-  }
-  __syncthreads();
-  const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
-      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
-  uint16_t* Cs = smem;
-  constexpr int kChunksPerRow = BN / 8;
-#pragma unroll 4
-  for (int c = tid; c < BM * kChunksPerRow; c += kWsThreads) {
-    const int r = c / kChunksPerRow, ch = c % kChunksPerRow;
-    const int gn = n0 + ch * 8;
-    if (gn < P.N) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(Cs + r * LDC + ch * 8);
-      __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)(m0 + r) * (uint32_t)P.N + (uint32_t)gn) * 2u, 0, 0);
+    if (kb == 0 && ke == nk) {
+      __syncthreads();  // the MFMA waves' bf16 tile is in LDS
+      store_chunks(m0, n0);
     }
-  }
+    __syncthreads();
+  });
 }
 
 hipError_t launch_ws(const GemmParams& P, int blocks, hipStream_t stream) {
@@ -854,7 +918,7 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
     P.upt = K / BK / P.ups;
     P.sk_tiles = P.tiles_m * P.tiles_n;
     P.U = (long long)P.sk_tiles * P.upt;
-    hipError_t e = launch_tiles<256, 256, true>(P, plan.G, stream);
+    hipError_t e = launch_ws(P, plan.G, stream);
     if (e != hipSuccess) return e;
     return launch_sk_reduce<256, 256>(P, plan.G, stream);
   }
