@@ -218,9 +218,10 @@ def test_reference_prefill_kernel_shapes(m, k, n):
 
 
 # 1800 x 5120 -> 4368: 144 whole 256 x 256 tiles with 8-group scale blocks (the role-split kernel),
-# a partial last row of tiles (8 rows) and a partial last column (16 columns).
+# a partial last row of tiles (8 rows) and a partial last column (16 columns); 1536 x 512 -> 8192:
+# the same kernel over the shortest K it takes (one 8-step scale block).
 @pytest.mark.parametrize("m,k,n", [(65, 1152, 1024), (255, 128, 528), (256, 256, 256), (257, 1024, 784),
-                                   (1024, 5120, 1040), (4096, 1024, 512), (1800, 5120, 4368)])
+                                   (1024, 5120, 1040), (4096, 1024, 512), (1800, 5120, 4368), (1536, 512, 8192)])
 def test_qmm_gemm_shapes(m, k, n):
     x, w, s, b = O.make_inputs(m, k, n, seed=m + k)
     check_qmm(gpu_qmm(x, w, s, b), O.quantized_matmul_exact(x, w, s, b), f"{m}x{k}x{n}", (x, w, s, b))
