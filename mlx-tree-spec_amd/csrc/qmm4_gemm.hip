@@ -510,13 +510,13 @@ hipError_t launch_tiles(const GemmParams& P, int blocks, hipStream_t stream) {
   return hipGetLastError();
 }
 
-// 256 x 256 tiles with K % 512 == 0 (whole, or stream-K segments), waves split by role: waves 0-7 (two per SIMD, the 2 x 4
-// wave grid and MFMA order of gemm_kernel, so the same bits) only read fragments and run MFMAs;
-// waves 8-11 (one per SIMD) only load, dequantize and store the next K step into the other LDS
-// stage. A SIMD overlaps one wave's MFMAs with another wave's VALU far better than MFMAs and VALU
-// interleaved inside one wave: a dequantization wave beside an MFMA wave ran in the time of the
-// dequantization alone, where waves mixing both ran in ~0.8 of the sum of the two. 12 waves share
-// the SIMDs' 512 registers per lane: at most 168 per wave (146 used).
+// 256 x 256 tiles with K % 512 == 0 (whole, or stream-K segments), waves split by role: waves 0-7
+// (two per SIMD, the 2 x 4 wave grid and MFMA order of gemm_kernel, so the same bits) only read
+// fragments and run MFMAs; waves 8-11 (one per SIMD) only load, dequantize and store the next K
+// step into the other LDS stage. A SIMD overlaps one wave's MFMAs with another wave's VALU far
+// better than MFMAs and VALU interleaved inside one wave: a dequantization wave beside an MFMA wave
+// ran in the time of the dequantization alone, where waves mixing both ran in ~0.8 of the sum of
+// the two. 12 waves share the SIMDs' 512 registers per lane: at most 168 per wave (154 used).
 // Producer thread pt (0-255): activation chunk pt % 8 of rows pt / 8 + 32 j (j < 8) and the 8 code
 // words (one group, 64 k) of column pt per K step, two steps ahead in registers; the column's scale
 // and bias come 8 groups per 16-byte load.
