@@ -231,18 +231,17 @@ void rowphase_kernel(RowPhaseParams P) {
     constexpr bool FAST = decltype(fast)::value;
     const u32x4* xb = xs(st);
     // Phase pw of the window: dwords pw * V .. pw * V + V - 1 of each row's window run.
-    const uint32_t* sb32 = reinterpret_cast<const uint32_t*>(ws_s) + pw * V;
-    const uint32_t* bb32 = reinterpret_cast<const uint32_t*>(ws_b) + pw * V;
-    // This lane's words of super-step v lie in group 2 v + g / 2 of the phase; dword v of row
-    // (wave + W j) * 16 + n holds groups 2 v and 2 v + 1.
+    // This lane's words of super-step v lie in group 2 v + g / 2 of the phase: bf16 2 v + g / 2 of
+    // row (wave + W j) * 16 + n's window run, read alone (a 16-bit LDS read) so that no half needs
+    // selecting in registers.
+    const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(ws_s) + pw * V * 2 + (g >> 1);
+    const uint16_t* bb16 = reinterpret_cast<const uint16_t*>(ws_b) + pw * V * 2 + (g >> 1);
     float c1[BPW], c2[BPW], bfv[BPW];
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
       const int lrow = 16 * (wave + kRpWaves * j) + n;
-      const uint32_t sd = sb32[lrow * (C::kWS / 4) + v];
-      const uint32_t bd = bb32[lrow * (C::kWS / 4) + v];
-      const uint32_t sbits = (g >> 1) ? (sd >> 16) : (sd & 0xFFFFu);
-      const uint32_t bbits = (g >> 1) ? (bd >> 16) : (bd & 0xFFFFu);
+      const uint32_t sbits = sb16[lrow * (C::kWS / 2) + 2 * v];
+      const uint32_t bbits = bb16[lrow * (C::kWS / 2) + 2 * v];
       const float sf = bf16_to_f32(sbits);
       bfv[j] = bf16_to_f32(bbits);
       c1[j] = FAST ? sf * 16777216.0f : sf;
