@@ -14,6 +14,8 @@
 //    (deterministic), one item per thread over the whole GPU.
 //  * Wave w owns blocks w, w + 8, w + 16, ... of the range (at most BPW) and holds one whole phase
 //    of their weights in registers while the next phase's weights are in flight (double buffer).
+//    Slots past a wave's blocks compute on zero weights (a straight-line loop), except that the
+//    wide plans' variants skip the last slot in the waves that hold no block there.
 //    Lane (n = lane % 16, g = lane / 16) loads V 16-byte pieces of row n of each block, piece v at
 //    byte 64 v + 16 g of the row's PH / 2-byte run, so each row is read as one contiguous run.
 //  * Word t of piece v holds k = PH p + 128 v + 32 g + 8 t: the B operand of MFMA 16x16x32 (v, t)
@@ -55,7 +57,7 @@ struct RowPhaseParams {
   int ranges;     // block ranges
 };
 
-template <int MB_, int V_, int BPW_, int W_, int STG_ = 3>
+template <int MB_, int V_, int BPW_, int W_, int STG_ = 3, bool OPT_ = false>
 struct RpCfg {
   static constexpr int kRpWaves = W_;  // waves per workgroup
   static constexpr int kRpThreads = 64 * W_;
@@ -65,6 +67,9 @@ struct RpCfg {
   static constexpr int PH = 128 * V;  // k per phase
   static constexpr int BPW = BPW_;    // blocks per wave (at most)
   static constexpr int RW = 16 * kRpWaves * BPW;  // rows per range (at most)
+  // The last block slot's arithmetic runs only in the waves that hold a BPW-th block (wide plans
+  // whose blocks leave some waves one short); otherwise every wave computes every slot.
+  static constexpr bool kOptLast = OPT_ && BPW > 1;
   static constexpr int kXPieces = V * 16 * MP;    // 16-byte x pieces per phase
   static constexpr int kSB = 4 * V;               // bytes of scales (or biases) per row and phase
   static constexpr int WP = 64 / kSB;             // phases per scale window (64 bytes of each row)
@@ -236,6 +241,8 @@ void rowphase_kernel(RowPhaseParams P) {
     // selecting in registers.
     const uint16_t* sb16 = reinterpret_cast<const uint16_t*>(ws_s) + pw * V * 2 + (g >> 1);
     const uint16_t* bb16 = reinterpret_cast<const uint16_t*>(ws_b) + pw * V * 2 + (g >> 1);
+    constexpr int NJ = C::kOptLast ? BPW - 1 : BPW;  // slots every wave computes
+    const bool full = !C::kOptLast || nbw == BPW;     // wave-uniform
     float c1[BPW], c2[BPW], bfv[BPW];
 #pragma unroll
     for (int j = 0; j < BPW; ++j) {
@@ -253,9 +260,11 @@ void rowphase_kernel(RowPhaseParams P) {
 #pragma unroll
       for (int i = 0; i < MB; ++i) a[i] = xb[(v * 16 + g * 4 + t) * MP + i * 16 + n];
       // Blocks past this wave's count hold zero weights (their loads lie outside the buffer)
-      // and sums that are never stored: computing them keeps the loop free of branches.
+      // and sums that are never stored: computing them keeps the loop free of branches, except
+      // for the last slot of an OPT variant, which only the waves holding a BPW-th block run.
 #pragma unroll
       for (int j = 0; j < BPW; ++j) {
+        if (j >= NJ && !full) continue;
         const u32x4 B = FAST ? dequant_word_fast(wv[J][j][v][t], c1[j], c2[j], bfv[j])
                              : dequant_word(wv[J][j][v][t], c1[j], c2[j], bfv[j]);
 #pragma unroll
@@ -470,40 +479,50 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
 
 }  // namespace
 
-// Kernel table: id -> (row blocks of x, super-steps per phase, blocks per wave, waves, x stages).
+// Kernel table: id -> (row blocks of x, super-steps per phase, blocks per wave, waves, x stages,
+// last slot computed only by the waves that hold a block there). Ids 20-23 are the wide plans'
+// twins of ids 4, 5, 10 and 2: over 34816 and 65984 columns (9 and 17 blocks per workgroup) the
+// waves short of a last block skip it, so the busiest SIMD runs 3 of 4 (5 of 6) block slots per
+// phase: 24-64 rows over 5120 -> 34816 / 65984 9-17% faster, identical bits.
 #define QMM4_ROWPHASE_VARIANTS(X) \
-  X(0, 1, 2, 5, 8, 3)             \
-  X(1, 2, 2, 5, 8, 3)             \
-  X(2, 4, 2, 3, 8, 3)             \
-  X(3, 1, 4, 2, 8, 3)             \
-  X(4, 2, 4, 2, 8, 3)             \
-  X(5, 4, 2, 2, 8, 3)             \
-  X(6, 1, 4, 1, 8, 3)             \
-  X(7, 2, 4, 1, 8, 3)             \
-  X(8, 4, 2, 1, 8, 3)             \
-  X(9, 1, 2, 3, 8, 3)             \
-  X(10, 2, 2, 3, 8, 3)            \
-  X(11, 1, 2, 4, 8, 3)            \
-  X(12, 2, 2, 4, 8, 3)            \
-  X(13, 5, 2, 2, 8, 2)            \
-  X(14, 5, 2, 1, 8, 2)            \
-  X(15, 6, 2, 2, 8, 2)            \
-  X(16, 6, 2, 1, 8, 2)            \
-  X(17, 7, 2, 2, 8, 2)            \
-  X(18, 7, 2, 1, 8, 2)            \
-  X(19, 8, 2, 1, 8, 2)
-constexpr int kRpVariants = 20;
+  X(0, 1, 2, 5, 8, 3, 0)          \
+  X(1, 2, 2, 5, 8, 3, 0)          \
+  X(2, 4, 2, 3, 8, 3, 0)          \
+  X(3, 1, 4, 2, 8, 3, 0)          \
+  X(4, 2, 4, 2, 8, 3, 0)          \
+  X(5, 4, 2, 2, 8, 3, 0)          \
+  X(6, 1, 4, 1, 8, 3, 0)          \
+  X(7, 2, 4, 1, 8, 3, 0)          \
+  X(8, 4, 2, 1, 8, 3, 0)          \
+  X(9, 1, 2, 3, 8, 3, 0)          \
+  X(10, 2, 2, 3, 8, 3, 0)         \
+  X(11, 1, 2, 4, 8, 3, 0)         \
+  X(12, 2, 2, 4, 8, 3, 0)         \
+  X(13, 5, 2, 2, 8, 2, 0)         \
+  X(14, 5, 2, 1, 8, 2, 0)         \
+  X(15, 6, 2, 2, 8, 2, 0)         \
+  X(16, 6, 2, 1, 8, 2, 0)         \
+  X(17, 7, 2, 2, 8, 2, 0)         \
+  X(18, 7, 2, 1, 8, 2, 0)         \
+  X(19, 8, 2, 1, 8, 2, 0)         \
+  X(20, 2, 4, 2, 8, 3, 1)         \
+  X(21, 4, 2, 2, 8, 3, 1)         \
+  X(22, 2, 2, 3, 8, 3, 1)         \
+  X(23, 4, 2, 3, 8, 3, 1)
+constexpr int kRpVariants = 24;
 
-#define QMM4_RPCFG(id, mb, v, bpw, w, stg) typedef RpCfg<mb, v, bpw, w, stg> RpCfg##id;
+#define QMM4_RPCFG(id, mb, v, bpw, w, stg, opt) typedef RpCfg<mb, v, bpw, w, stg, opt> RpCfg##id;
 QMM4_ROWPHASE_VARIANTS(QMM4_RPCFG)
 #undef QMM4_RPCFG
 
-static bool rowphase_geometry(int id, int* mb, int* v, int* bpw, size_t* lds, int* items, int* waves = nullptr) {
+static bool rowphase_geometry(int id, int* mb, int* v, int* bpw, size_t* lds, int* items, int* waves = nullptr,
+                              bool* opt = nullptr) {
   switch (id) {
-#define QMM4_RPG(i, m, vv, b, w, stg)                                                                 \
+#define QMM4_RPG(i, m, vv, b, w, stg, op)                                                                \
   case i:                                                                                           \
     *mb = m; *v = vv; *bpw = b; *lds = RpCfg##i::kLds; *items = RpCfg##i::kItems;                    \
     if (waves) *waves = w;                                                                          \
+    if (opt) *opt = op;                                                                             \
     return true;
     QMM4_ROWPHASE_VARIANTS(QMM4_RPG)
 #undef QMM4_RPG
@@ -513,7 +532,7 @@ static bool rowphase_geometry(int id, int* mb, int* v, int* bpw, size_t* lds, in
 
 static const void* rowphase_func(int id) {
   switch (id) {
-#define QMM4_RPF(i, m, vv, b, w, stg) \
+#define QMM4_RPF(i, m, vv, b, w, stg, opt) \
   case i: return reinterpret_cast<const void*>(&rowphase_kernel<RpCfg##i>);
     QMM4_ROWPHASE_VARIANTS(QMM4_RPF)
 #undef QMM4_RPF
@@ -539,10 +558,11 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   auto pick = [&](int want) {
     int id = -1, best_b = 0;
     for (int c = 0; c < kRpVariants; ++c) {
-      int cm, cv, cb, items;
+      int cm, cv, cb, items, cw;
       size_t l;
-      rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
-      if (cm != mb || ks % cv != 0) continue;
+      bool co;
+      rowphase_geometry(c, &cm, &cv, &cb, &l, &items, &cw, &co);
+      if (cm != mb || ks % cv != 0 || co) continue;
       const bool fits = cb >= want;
       const bool best_fits = best_b >= want;
       if (id < 0 || (fits && (!best_fits || cb < best_b)) || (!fits && !best_fits && cb > best_b)) {
@@ -563,10 +583,11 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
     const int maxb = [&] {
       int m = 0;
       for (int c = 0; c < kRpVariants; ++c) {
-        int cm, cv, cb, items;
+        int cm, cv, cb, items, cw;
         size_t l;
-        rowphase_geometry(c, &cm, &cv, &cb, &l, &items);
-        if (cm == mb && ks % cv == 0 && cb > m) m = cb;
+        bool co;
+        rowphase_geometry(c, &cm, &cv, &cb, &l, &items, &cw, &co);
+        if (cm == mb && ks % cv == 0 && !co && cb > m) m = cb;
       }
       return m;
     }();
@@ -618,6 +639,22 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
     }
   }
   if (id < 0) return false;
+  if (wide) {
+    // A wide plan whose blocks leave some waves a slot short takes the variant that skips that
+    // slot's arithmetic in those waves, where one is built.
+    int cm0, cv0, cb0, items0, cw0;
+    size_t l0;
+    rowphase_geometry(id, &cm0, &cv0, &cb0, &l0, &items0, &cw0);
+    const int bwp = bw < kW * cb0 ? bw : kW * cb0;
+    if (bwp < kW * cb0)
+      for (int c = 0; c < kRpVariants; ++c) {
+        int cm, cv, cb, items, cw;
+        size_t l;
+        bool co;
+        rowphase_geometry(c, &cm, &cv, &cb, &l, &items, &cw, &co);
+        if (co && cm == cm0 && cv == cv0 && cb == cb0 && cw == cw0) id = c;
+      }
+  }
   int cm, v, bpw, items;
   size_t lds;
   rowphase_geometry(id, &cm, &v, &bpw, &lds, &items);
@@ -657,7 +694,7 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
   if (e != hipSuccess) return e;
   // K split: the reduce kernel's grid has one thread per f32x4 item of every range's tile.
   switch (plan.variant) {
-#define QMM4_RPL(i, m, vv, bb, w, stg)                                                                       \
+#define QMM4_RPL(i, m, vv, bb, w, stg, opt)                                                                   \
   case i:                                                                                                   \
     hipLaunchKernelGGL(rowphase_kernel<RpCfg##i>, dim3(plan.blocks), dim3(RpCfg##i::kRpThreads), plan.lds,   \
                        stream, P);                                                                          \

@@ -16,6 +16,9 @@ Routes of 65-128 rows (qmm4_affine_bf16, dispatch_qmm):
                rows, or 128 over at most 2048 columns, when K % 512 == 0 and N leaves the kernel's
                plan narrow (a wide plan, N >= 32768 on 256 CUs, goes to the GEMM);
   "gemm"       the GEMM (stream-K over 128 x 128 tiles at these rows).
+Row-phase variants of wide plans (qmm4_affine_bf16 at 17-64 rows over N >= 32768): "opt" is a
+variant whose waves without a block in the last slot skip that slot's arithmetic (9 or 17 blocks
+per workgroup leave most waves a block short); "full" computes every slot in every wave.
 Routes of the gate+up SiLU·mul projection (qmm4_gate_up_silu_bf16):
   "fused"     one row-split launch with the epilogue fused;
   "two-pass"  the projection into the library's scratch, then the SiLU·mul pass (no fused
@@ -76,4 +79,14 @@ MID_ROW_CASES = [
     (128, 17408, 5120, "gemm"),
     (72, 34816, 5120, "gemm"),        # a wide row-phase plan
     (96, 1024, 640, "gemm"),          # K % 512 != 0
+]
+
+# (M, N, K, variant form)
+ROWPHASE_WIDE_CASES = [
+    (24, 34816, 5120, "opt"),   # 9 blocks per workgroup, 2 slots per wave (phases of 512 k)
+    (33, 32784, 2048, "opt"),   # 64-row x blocks, a partial last range
+    (48, 33024, 3072, "opt"),
+    (32, 65984, 2048, "opt"),   # 17 blocks, 3 slots per wave
+    (64, 65984, 2048, "opt"),   # 64-row x blocks over the drafter's head
+    (32, 131072, 2048, "full"),  # 32 blocks: every wave holds 4
 ]

@@ -22,7 +22,7 @@ import golden_io
 from mlx_tree_spec_amd import STATS, QuantizedLinear, dequantize, install, quantized_matmul
 from oracle import cpu
 from oracle import qmm4_oracle as O
-from route_cases import MID_ROW_CASES
+from route_cases import MID_ROW_CASES, ROWPHASE_WIDE_CASES
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -693,13 +693,27 @@ def test_rowphase_shapes(m, k, n):
     check_qmm(gpu_qmm(x, w, s, b), workload_ref(x, w, s, b), f"row-phase {m}x{k}x{n}", (x, w, s, b))
 
 
+# Wide row-phase plans whose blocks leave most waves a block short take variants that skip the
+# last slot's arithmetic in those waves (route_cases.ROWPHASE_WIDE_CASES; the variant of each case
+# is checked against the planner in tests/test_plans.py).
+@pytest.mark.parametrize("m,n,k,form", ROWPHASE_WIDE_CASES)
+def test_rowphase_wide_shapes(m, n, k, form):
+    note(f"row-phase wide ({form}) {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 17 + k + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"row-phase wide {m}x{k}x{n}", (x, w, s, b))
+    assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 @pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48), (65984, 16), (131072, 32), (4096, 80), (2064, 112),
-                                 (1024, 128)])
+                                 (1024, 128), (33024, 48), (65984, 32), (65984, 64)])
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
     """One-hot rows of x on the row-phase path (wide and K-split): each output is one dequantized
     weight and must equal the oracle's bit for bit, for scale windows dequantized in the fast
-    form, in the general form, and for a mix of the two."""
+    form, in the general form, and for a mix of the two. 32800 / 33024 columns at 32 / 48 rows and
+    65984 at 32 and 64 rows take the wide variants whose short waves skip the last block slot."""
     k = 2048
     rng = np.random.default_rng({"fast": 21, "mixed": 22, "slow": 23}[kind] + n)
     s, b = scale_bias_pairs(kind, n * (k // 64), rng)

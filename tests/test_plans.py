@@ -95,3 +95,15 @@ def test_mid_row_cases_take_their_routes(planner_exe):
         rows_ok = m <= 112 or (m <= 128 and n <= 2048)
         takes = rows_ok and k % 512 == 0 and isinstance(p, dict) and p["wide"] == "0"
         assert route == ("row-phase" if takes else "gemm"), (m, n, k, route, p)
+
+
+def test_rowphase_wide_cases_take_their_variants(planner_exe):
+    """Each wide row-phase shape of test_gpu_parity.py reaches the variant form its label names on
+    256 CUs: a variant whose short waves skip the last block slot ("opt", ids 20-23 of the kernel
+    table) or one that computes every slot ("full")."""
+    from route_cases import CUS, ROWPHASE_WIDE_CASES
+
+    lines = [f"rowphase {m} {n} {k} {CUS}" for m, n, k, _ in ROWPHASE_WIDE_CASES]
+    for (m, n, k, form), p in zip(ROWPHASE_WIDE_CASES, query(planner_exe, lines)):
+        assert isinstance(p, dict) and p["wide"] == "1" and p["S"] == "1", (m, n, k, p)
+        assert (20 <= int(p["variant"]) <= 23) == (form == "opt"), (m, n, k, form, p)
