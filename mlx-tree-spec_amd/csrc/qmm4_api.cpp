@@ -339,8 +339,12 @@ int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, cons
 // interleaved rounds, the model's up and down projections): 65 / 80 / 96 / 112 rows 38.5 / 40.2 /
 // 44.2 / 47.4 us against 46.7 / 47.2 / 48.5 / 48.6 us (5120 -> 17408), 35.8 / 36.7 / 40.4 / 44.2
 // against 45.5 / 46.5 / 47.8 / 48.8 (17408 -> 5120); at 120-128 rows (one block per wave) 53-74
-// against 48-51 us, but 128 x 5120 -> 1024 17.3 against 47.6 us.
+// against 48-51 us, but 128 x 5120 -> 1024 17.3 against 47.6 us. A wide plan (every workgroup its
+// own blocks over all of K) is taken up to kRowPhaseMaxMWide rows when it needs at most one range
+// per CU: 65 / 80 / 96 x 5120 -> 34816 57.5 / 64.5 / 71.9 us against 71.8 / 73.3 / 73.5 us on the
+// GEMM, 72 x 4096 -> 32768 43.6 against 50.1 us; at 112 rows 80.8 against 74.5 us.
 constexpr int kRowPhaseMaxM = 112;
+constexpr int kRowPhaseMaxMWide = 96;
 constexpr int kRowPhaseMaxMNarrow = 128;
 constexpr int kRowPhaseNarrowN = 2048;
 
@@ -368,12 +372,15 @@ int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* s
 
   if (M > 64) {
     // 65-112 rows over a small N (a verify batch past 64 tree nodes, a short prompt tail): the
-    // row-phase kernel with 80-112-row x blocks, K split over the CUs. Its weights are dequantized
-    // once for all rows, where the GEMM's 128-row tiles pad these rows to 128.
+    // row-phase kernel with 80-112-row x blocks, K split over the CUs; up to 96 rows also a wide
+    // plan of at most one range per CU (the MLP's 34816-column gate+up). Its weights are
+    // dequantized once for all rows, where the GEMM's 128-row tiles pad these rows to 128.
     if ((M <= kRowPhaseMaxM || (M <= kRowPhaseMaxMNarrow && N <= kRowPhaseNarrowN)) && aligned(scales, 16) &&
         aligned(biases, 16) && K % 512 == 0) {
       RowPhasePlan pplan;
-      if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) && !pplan.wide) return run_rowphase(pplan);
+      if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan) &&
+          (!pplan.wide || (M <= kRowPhaseMaxMWide && pplan.ranges <= di->cus)))
+        return run_rowphase(pplan);
     }
     GemmPlan gplan;
     gemm_plan((int)M, (int)N, (int)K, di->cus, ws.capacity(), sb, bb, &gplan);

@@ -14,7 +14,8 @@ Routes of the residual add + RMS norm folded into the projection (qmm4_add_rms_n
 Routes of 65-128 rows (qmm4_affine_bf16, dispatch_qmm):
   "row-phase"  the row-phase kernel with 80-128-row x blocks and K split over the CUs: up to 112
                rows, or 128 over at most 2048 columns, when K % 512 == 0 and N leaves the kernel's
-               plan narrow (a wide plan, N >= 32768 on 256 CUs, goes to the GEMM);
+               plan narrow; a wide plan (N >= 32768 on 256 CUs, every workgroup its own blocks
+               over all of K) up to 96 rows when it needs at most one range per CU;
   "gemm"       the GEMM (stream-K over 128 x 128 tiles at these rows).
 Row-phase variants of wide plans (qmm4_affine_bf16 at 17-64 rows over N >= 32768): "opt" is a
 variant whose waves without a block in the last slot skip that slot's arithmetic (9 or 17 blocks
@@ -77,7 +78,10 @@ MID_ROW_CASES = [
     (128, 1024, 5120, "row-phase"),   # 128-row blocks over a small N
     (113, 5120, 17408, "gemm"),
     (128, 17408, 5120, "gemm"),
-    (72, 34816, 5120, "gemm"),        # a wide row-phase plan
+    (72, 34816, 5120, "row-phase"),   # a wide plan, 9 blocks per workgroup (the 80-row twin)
+    (96, 34816, 5120, "row-phase"),   # the 96-row twin
+    (112, 34816, 5120, "gemm"),       # a wide plan past 96 rows
+    (72, 65984, 5120, "gemm"),        # a wide plan needing more ranges than CUs
     (96, 1024, 640, "gemm"),          # K % 512 != 0
 ]
 

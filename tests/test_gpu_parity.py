@@ -707,13 +707,14 @@ def test_rowphase_wide_shapes(m, n, k, form):
 
 
 @pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48), (65984, 16), (131072, 32), (4096, 80), (2064, 112),
-                                 (1024, 128), (33024, 48), (65984, 32), (65984, 64)])
+                                 (1024, 128), (33024, 48), (65984, 32), (65984, 64), (34816, 72), (34816, 96)])
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
     """One-hot rows of x on the row-phase path (wide and K-split): each output is one dequantized
     weight and must equal the oracle's bit for bit, for scale windows dequantized in the fast
-    form, in the general form, and for a mix of the two. 32800 / 33024 columns at 32 / 48 rows and
-    65984 at 32 and 64 rows take the wide variants whose short waves skip the last block slot."""
+    form, in the general form, and for a mix of the two. 32800 / 33024 columns at 32 / 48 rows,
+    65984 at 32 and 64 rows and 34816 at 72 and 96 rows take the wide variants whose short waves
+    skip the last block slot."""
     k = 2048
     rng = np.random.default_rng({"fast": 21, "mixed": 22, "slow": 23}[kind] + n)
     s, b = scale_bias_pairs(kind, n * (k // 64), rng)

@@ -87,13 +87,15 @@ def test_gate_up_cases_take_their_routes(planner_exe):
 def test_mid_row_cases_take_their_routes(planner_exe):
     """Each 65-128-row shape of test_gpu_parity.py reaches its route on 256 CUs: the row-phase
     kernel when dispatch_qmm's condition holds (up to 112 rows, or 128 over at most 2048 columns;
-    K % 512 == 0; a narrow row-phase plan), else the GEMM."""
+    K % 512 == 0; a narrow row-phase plan, or up to 96 rows a wide one of at most one range per
+    CU), else the GEMM."""
     from route_cases import CUS, MID_ROW_CASES
 
     lines = [f"rowphase {m} {n} {k} {CUS}" for m, n, k, _ in MID_ROW_CASES]
     for (m, n, k, route), p in zip(MID_ROW_CASES, query(planner_exe, lines)):
         rows_ok = m <= 112 or (m <= 128 and n <= 2048)
-        takes = rows_ok and k % 512 == 0 and isinstance(p, dict) and p["wide"] == "0"
+        plan_ok = isinstance(p, dict) and (p["wide"] == "0" or (m <= 96 and int(p["blocks"]) <= CUS))
+        takes = rows_ok and k % 512 == 0 and plan_ok
         assert route == ("row-phase" if takes else "gemm"), (m, n, k, route, p)
 
 
