@@ -216,8 +216,29 @@ int query() {
   return 0;
 }
 
+// Every planner's checks on the shapes read from stdin ("M N K" each), at 256, 304 and 80 CUs.
+void check_all(int M, int N, int K, int cus) {
+  if (M <= 16) {
+    check_rowsplit(M, N, K, cus, false);
+    if (N % 32 == 0) check_rowsplit(M, N, K, cus, true);
+    check_xreg(M, N, K, cus);
+  }
+  if (M <= 128) check_rowphase(M, N, K, cus);
+  if (M <= 64) check_verify(M, N, K, cus);
+  else check_gemm(M, N, K, cus);
+}
+
+int check_listed() {
+  int M, N, K;
+  while (std::scanf("%d %d %d", &M, &N, &K) == 3)
+    for (int cus : {256, 304, 80}) check_all(M, N, K, cus);
+  std::printf("plans checked: %lld, violations: %lld\n", g_checked, g_fail);
+  return g_fail > 255 ? 255 : (int)g_fail;
+}
+
 int main(int argc, char** argv) {
   if (argc > 1 && std::string(argv[1]) == "query") return query();
+  if (argc > 1 && std::string(argv[1]) == "check") return check_listed();
   const int Ms[] = {1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 15, 16, 17, 24, 32, 33, 48, 63, 64, 65, 80, 81, 96, 97, 112, 113,
                     128, 300, 1024, 4096};
   const int Ns[] = {16, 32, 48, 256, 1024, 1040, 2048, 3072, 4096, 4112, 5120, 6144, 10240, 12288,
@@ -227,16 +248,7 @@ int main(int argc, char** argv) {
   for (int cus : CUs)
     for (int M : Ms)
       for (int N : Ns)
-        for (int K : Ks) {
-          if (M <= 16) {
-            check_rowsplit(M, N, K, cus, false);
-            if (N % 32 == 0) check_rowsplit(M, N, K, cus, true);
-            check_xreg(M, N, K, cus);
-          }
-          if (M <= 128) check_rowphase(M, N, K, cus);
-          if (M <= 64) check_verify(M, N, K, cus);
-          else check_gemm(M, N, K, cus);
-        }
+        for (int K : Ks) check_all(M, N, K, cus);
   std::printf("plans checked: %lld, violations: %lld\n", g_checked, g_fail);
   return g_fail > 255 ? 255 : (int)g_fail;
 }

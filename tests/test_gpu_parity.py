@@ -347,6 +347,34 @@ def test_model_linear_shapes(k, n, rows):
         check_qmm(y, workload_ref(xm, w, s, b), f"model linear {m}x{k}x{n}", (xm, w, s, b))
 
 
+# Shapes drawn at random (seeded; kept here as a list so the set does not depend on the generator's
+# version): rows from each band the dispatcher distinguishes (decode 1-4, small verify 5-16, verify
+# 17-64, mid 65-300), K any multiple of 128 up to 8192 (so K % 512 is often not 0: other unit
+# sizes, the verify and skinny kernels, the GEMM's 2-byte scale loads), N any multiple of 16 up to
+# 41600 (partial ranges, tiles and blocks everywhere), at most 1.2e9 multiply-adds each. Every route
+# and plan the planners give these shapes must match the oracle and repeat its bits.
+RANDOM_SHAPES = [(4, 1536, 1104), (3, 3072, 19440), (1, 3072, 26768), (2, 6912, 32896), (3, 7424, 30016),
+                 (1, 7040, 27168), (1, 2560, 6896), (4, 6016, 38272), (2, 5248, 25136), (4, 1024, 21440),
+                 (3, 6784, 27296), (2, 3840, 14096), (6, 2304, 6080), (7, 7040, 21888), (5, 3584, 11280),
+                 (12, 6912, 544), (8, 1408, 8144), (9, 4992, 13600), (9, 5504, 12480), (16, 1792, 38912),
+                 (11, 4992, 8608), (9, 3456, 37472), (5, 2688, 16992), (12, 3456, 13056), (17, 2176, 4400),
+                 (17, 3072, 14928), (63, 3968, 1424), (17, 384, 33040), (31, 768, 7280), (31, 512, 10672),
+                 (20, 896, 39408), (24, 256, 1568), (20, 5504, 2496), (33, 768, 3872), (31, 128, 35392),
+                 (48, 640, 27440), (100, 640, 11840), (100, 256, 27296), (65, 3584, 3504), (100, 640, 4912),
+                 (72, 128, 14688), (80, 384, 4736), (129, 1280, 5312), (112, 1152, 7648), (65, 384, 22736),
+                 (160, 5376, 944), (65, 896, 11728), (256, 5376, 640)]
+
+
+@pytest.mark.parametrize("m,k,n", RANDOM_SHAPES)
+def test_random_shapes(m, k, n):
+    note(f"random shape {m}x{k}x{n}")
+    x, w, s, b = O.make_inputs(m, k, n, sigma=0.5 if k > 6144 else 1.0, seed=m * 7919 + k * 31 + n)
+    xd, wd, sd, bd = bf16_dev(x), u32_dev(w), bf16_dev(s), bf16_dev(b)
+    y = host_bits(quantized_matmul(xd, wd, sd, bd))
+    check_qmm(y, workload_ref(x, w, s, b), f"random {m}x{k}x{n}", (x, w, s, b))
+    assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
+
+
 @pytest.mark.parametrize("m,k,n", [(3, 192, 64), (70, 320, 48), (5, 128, 24), (1, 5120, 1000), (200, 64, 40)])
 def test_qmm_general_shapes(m, k, n):
     note(f"general shape {m}x{k}x{n}")

@@ -109,3 +109,18 @@ def test_rowphase_wide_cases_take_their_variants(planner_exe):
     for (m, n, k, form), p in zip(ROWPHASE_WIDE_CASES, query(planner_exe, lines)):
         assert isinstance(p, dict) and p["wide"] == "1" and p["S"] == "1", (m, n, k, p)
         assert (20 <= int(p["variant"]) <= 23) == (form == "opt"), (m, n, k, form, p)
+
+
+def test_random_shapes_keep_kernel_invariants(planner_exe):
+    """The seeded random shapes of test_gpu_parity.py (RANDOM_SHAPES) pass every planner's checks
+    at 256, 304 and 80 CUs before any of them runs on a GPU."""
+    import ast
+
+    src = open(os.path.join(ROOT, "tests", "test_gpu_parity.py")).read()
+    start = src.index("RANDOM_SHAPES = ")
+    shapes = ast.literal_eval(src[start + len("RANDOM_SHAPES = "):src.index("]", start) + 1])
+    assert len(shapes) >= 40
+    run = subprocess.run([planner_exe, "check"], input="".join(f"{m} {n} {k}\n" for m, k, n in shapes),
+                         capture_output=True, text=True, timeout=60)
+    assert run.returncode == 0, run.stdout[-4000:] + run.stderr[-2000:]
+    assert "violations: 0" in run.stdout
