@@ -480,10 +480,10 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
 }  // namespace
 
 // Kernel table: id -> (row blocks of x, super-steps per phase, blocks per wave, waves, x stages,
-// last slot computed only by the waves that hold a block there). Ids 20-25 are the wide plans'
-// twins of ids 4, 5, 10, 2, 13 and 15: over 34816 and 65984 columns (9 and 17 blocks per
+// last slot computed only by the waves that hold a block there). Ids 20-27 are the wide plans'
+// twins of ids 4, 5, 10, 2, 13, 15, 9 and 3: over 34816 and 65984 columns (9 and 17 blocks per
 // workgroup) the waves short of a last block skip it, so the busiest SIMD runs 3 of 4 (5 of 6)
-// block slots per phase: 24-64 rows over 5120 -> 34816 / 65984 9-17% faster, identical bits; 65-96
+// block slots per phase: 9-64 rows over 5120 -> 34816 / 65984 9-17% faster, identical bits; 65-96
 // rows over 34816 (ids 24, 25) then beat the GEMM.
 #define QMM4_ROWPHASE_VARIANTS(X) \
   X(0, 1, 2, 5, 8, 3, 0)          \
@@ -511,8 +511,10 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
   X(22, 2, 2, 3, 8, 3, 1)         \
   X(23, 4, 2, 3, 8, 3, 1)         \
   X(24, 5, 2, 2, 8, 2, 1)         \
-  X(25, 6, 2, 2, 8, 2, 1)
-constexpr int kRpVariants = 26;
+  X(25, 6, 2, 2, 8, 2, 1)         \
+  X(26, 1, 2, 3, 8, 3, 1)         \
+  X(27, 1, 4, 2, 8, 3, 1)
+constexpr int kRpVariants = 28;
 
 #define QMM4_RPCFG(id, mb, v, bpw, w, stg, opt) typedef RpCfg<mb, v, bpw, w, stg, opt> RpCfg##id;
 QMM4_ROWPHASE_VARIANTS(QMM4_RPCFG)

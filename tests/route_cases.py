@@ -94,3 +94,18 @@ ROWPHASE_WIDE_CASES = [
     (64, 65984, 2048, "opt"),   # 64-row x blocks over the drafter's head
     (32, 131072, 2048, "full"),  # 32 blocks: every wave holds 4
 ]
+
+# Shapes of the row-phase tests in test_gpu_parity.py, each of which dispatch_qmm must send to the
+# row-phase kernel (checked in tests/test_plans.py against the built planners, in dispatch order).
+# (M, K, N): wide and K-split plans, 9-16 rows where no row-split plan fits (x of 16 rows over
+# K = 5120 leaves no LDS for a vocabulary head's unit slots), partial ranges and windows.
+ROWPHASE_SHAPES = [(17, 5120, 4096), (33, 2048, 32784), (9, 5120, 65984), (48, 3072, 33024), (64, 1024, 2064),
+                   (24, 17408, 1024), (16, 5120, 65984), (32, 2048, 65984), (16, 5120, 99984), (32, 2048, 131072),
+                   (24, 5120, 17408), (12, 17408, 5120), (48, 6144, 5120), (32, 2048, 8192)]
+# (N, M, K) of the one-hot exact-dequantization test.
+ROWPHASE_ONE_HOT = [(32800, 32, 2048), (2064, 48, 2048), (65984, 16, 5120), (131072, 32, 2048), (4096, 80, 2048),
+                    (2064, 112, 2048), (1024, 128, 2048), (33024, 48, 2048), (65984, 32, 2048), (65984, 64, 2048),
+                    (34816, 72, 2048), (34816, 96, 2048)]
+# (M, K, N) of the scale-window form switches.
+ROWPHASE_WINDOW_CASES = [(12, 5120, 65552), (48, 3072, 33024), (64, 17408, 5120), (32, 5120, 65552),
+                         (96, 17408, 5120)]

@@ -22,7 +22,8 @@ import golden_io
 from mlx_tree_spec_amd import STATS, QuantizedLinear, dequantize, install, quantized_matmul
 from oracle import cpu
 from oracle import qmm4_oracle as O
-from route_cases import MID_ROW_CASES, ROWPHASE_WIDE_CASES
+from route_cases import (MID_ROW_CASES, ROWPHASE_ONE_HOT, ROWPHASE_SHAPES, ROWPHASE_WIDE_CASES,
+                         ROWPHASE_WINDOW_CASES)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -711,10 +712,7 @@ def test_rowsplit_xreg_one_hot_is_exact_dequant(kind):
 # 24 rows over 5120 -> 17408: K split over ranges of 3 blocks per wave (46 ranges x 5 slices).
 # Ranges of one block per wave where two would leave a workgroup at most 3 phases: 12 x 17408 ->
 # 5120 (40 ranges x 6 slices of 6 phases), 48 x 6144 -> 5120 (4 phases), 32 x 2048 -> 8192.
-@pytest.mark.parametrize("m,k,n", [(17, 5120, 4096), (33, 2048, 32784), (8, 5120, 34848), (48, 3072, 33024),
-                                   (64, 1024, 2064), (24, 17408, 1024), (16, 5120, 65984), (32, 2048, 65984),
-                                   (16, 5120, 99984), (32, 2048, 131072), (24, 5120, 17408), (12, 17408, 5120),
-                                   (48, 6144, 5120), (32, 2048, 8192)])
+@pytest.mark.parametrize("m,k,n", ROWPHASE_SHAPES)
 def test_rowphase_shapes(m, k, n):
     note(f"row-phase {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, seed=m * 11 + k + n)
@@ -734,16 +732,14 @@ def test_rowphase_wide_shapes(m, n, k, form):
     assert np.array_equal(host_bits(quantized_matmul(xd, wd, sd, bd)), y)
 
 
-@pytest.mark.parametrize("n,m", [(32800, 32), (2064, 48), (65984, 16), (131072, 32), (4096, 80), (2064, 112),
-                                 (1024, 128), (33024, 48), (65984, 32), (65984, 64), (34816, 72), (34816, 96)])
+@pytest.mark.parametrize("n,m,k", ROWPHASE_ONE_HOT)
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
-def test_rowphase_one_hot_is_exact_dequant(kind, n, m):
+def test_rowphase_one_hot_is_exact_dequant(kind, n, m, k):
     """One-hot rows of x on the row-phase path (wide and K-split): each output is one dequantized
     weight and must equal the oracle's bit for bit, for scale windows dequantized in the fast
     form, in the general form, and for a mix of the two. 32800 / 33024 columns at 32 / 48 rows,
-    65984 at 32 and 64 rows and 34816 at 72 and 96 rows take the wide variants whose short waves
-    skip the last block slot."""
-    k = 2048
+    65984 at 16, 32 and 64 rows and 34816 at 72 and 96 rows take the wide variants whose short
+    waves skip the last block slot."""
     rng = np.random.default_rng({"fast": 21, "mixed": 22, "slow": 23}[kind] + n)
     s, b = scale_bias_pairs(kind, n * (k // 64), rng)
     s, b = s.reshape(n, k // 64), b.reshape(n, k // 64)
@@ -778,12 +774,13 @@ def test_mid_rows(m, n, k, route):
 
 # Scale windows of the row-phase kernel are 32 groups (2048 values of k) of every row. Odd windows
 # here hold scales that need the general form, even windows only fast-form scales, so a workgroup
-# whose phases cross windows switches form at each window: wide ranges of 10 and 12 phases over 3
-# and 2 windows (windows loaded a phase ahead), the K-split batched-verify shape (ranges of 5-6
-# phases, some across a window edge), and a wide 32-row shape whose variant stages each window at
-# its first phase (5 blocks per wave leave no registers for a window ahead).
-@pytest.mark.parametrize("m,k,n", [(8, 5120, 34848), (48, 3072, 33024), (64, 17408, 5120), (32, 5120, 65552),
-                                   (96, 17408, 5120)])
+# whose phases cross windows switches form at each window: wide ranges of 20 and 12 phases over 3
+# and 2 windows (12 rows over 65552 columns on the one-row-block twin that skips short waves' last
+# slot; 48 rows over 33024 with windows loaded a phase ahead), the K-split batched-verify shape
+# (ranges of 5-6 phases, some across a window edge), a wide 32-row shape whose variant stages each
+# window at its first phase (5 blocks per wave leave no registers for a window ahead), and 96 rows
+# (two x stages).
+@pytest.mark.parametrize("m,k,n", ROWPHASE_WINDOW_CASES)
 def test_rowphase_window_form_switches(m, k, n):
     note(f"row-phase window switches {m}x{k}x{n}")
     rng = np.random.default_rng(m * 7 + k)

@@ -124,3 +124,45 @@ def test_random_shapes_keep_kernel_invariants(planner_exe):
                          capture_output=True, text=True, timeout=60)
     assert run.returncode == 0, run.stdout[-4000:] + run.stderr[-2000:]
     assert "violations: 0" in run.stdout
+
+
+def dispatch_route(exe, cases):
+    """dispatch_qmm's route for each (M, N, K) on 256 CUs with 16-byte aligned scales, from the
+    built planners queried in dispatch order: past 64 rows the row-phase kernel (narrow plans up to
+    112 rows or 128 over at most 2048 columns, wide plans of at most one range per CU up to 96
+    rows) else the GEMM; up to 64 rows the x-in-registers row-split form (9-16 rows), the row-split
+    kernel, the row-phase kernel (from 5 rows when its plan is wide, has 17+ rows or fills half the
+    CUs), else the verify or skinny kernel ("other")."""
+    from route_cases import CUS
+
+    kinds = ("rowphase", "xreg", "rowsplit")
+    lines = [f"{kind} {m} {n} {k} {CUS}" for m, n, k in cases for kind in kinds]
+    out = query(exe, lines)
+    routes = []
+    for i, (m, n, k) in enumerate(cases):
+        rp, xr, rs = out[3 * i:3 * i + 3]
+        rp_ok = isinstance(rp, dict) and k % 512 == 0
+        if m > 64:
+            rows_ok = m <= 112 or (m <= 128 and n <= 2048)
+            wide_ok = rp_ok and (rp["wide"] == "0" or (m <= 96 and int(rp["blocks"]) <= CUS))
+            routes.append("row-phase" if rows_ok and wide_ok else "gemm")
+        elif m >= 9 and xr != "none":
+            routes.append("xreg")
+        elif rs != "none":
+            routes.append("row-split")
+        elif m >= 5 and rp_ok and (rp["wide"] == "1" or m >= 17 or 2 * int(rp["blocks"]) >= CUS):
+            routes.append("row-phase")
+        else:
+            routes.append("other")
+    return routes
+
+
+def test_rowphase_test_shapes_reach_the_rowphase_kernel(planner_exe):
+    """Every shape of the row-phase tests in test_gpu_parity.py (shapes, one-hot exact dequant,
+    window form switches, the wide variants) is sent to the row-phase kernel by dispatch_qmm."""
+    from route_cases import ROWPHASE_ONE_HOT, ROWPHASE_SHAPES, ROWPHASE_WIDE_CASES, ROWPHASE_WINDOW_CASES
+
+    cases = ([(m, n, k) for m, k, n in ROWPHASE_SHAPES] + [(m, n, k) for n, m, k in ROWPHASE_ONE_HOT]
+             + [(m, n, k) for m, k, n in ROWPHASE_WINDOW_CASES] + [(m, n, k) for m, n, k, _ in ROWPHASE_WIDE_CASES])
+    for case, route in zip(cases, dispatch_route(planner_exe, cases)):
+        assert route == "row-phase", (case, route)
