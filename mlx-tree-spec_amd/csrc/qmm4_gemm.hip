@@ -8,7 +8,7 @@
 // Geometry: BM = BN = 256, BK = 64 (one quantization group per K step), 8 waves in a 2 x 4
 // arrangement (two per SIMD, so one wave's loads, dequantization and LDS stores overlap the
 // other's MFMAs), each wave a 128 x 64 block of 4 x 2 MFMA 32x32x16 tiles (64 x 32 in the 128 x 128
-// tiles of stream-K and tail launches). LDS holds two stages of [BM][64 + 8] bf16 for the
+// tiles of stream-K and tail launches, 64 x 64 in the 128 x 256 tiles of stream-K launches). LDS holds two stages of [BM][64 + 8] bf16 for the
 // activations and [BN][64 + 8] for the dequantized weights (147 KB at 256 x 256); the 144-byte
 // row pitch keeps the 16-byte fragment reads free of bank conflicts.
 //
@@ -31,11 +31,11 @@
 //    tiles are walked in groups of 4 row tiles, so a group shares weight and activation blocks in
 //    L2.
 //  * At most one 128 x 128 tile per CU (65-256 rows of the model's projections): stream-K over
-//    128 x 128 tiles. The tiles x K units are split evenly over every resident workgroup (one per
-//    CU, with a 4-step register ring when K % 512 == 0: 65-128 rows 2-6% faster than two per CU
-//    with a 2-step ring); a workgroup's first and last segments may cover part of a tile and leave fp32 partial
-//    tiles, which gemm_sk_reduce_kernel adds in K order (the same bits whichever workgroup ran a
-//    segment).
+//    128 x 128 tiles, or 128 x 256 past 128 rows or for K >= 8192 (with 8-group scale blocks). The
+//    tiles x K units are split evenly over every resident workgroup (one per CU, with a 4-step
+//    register ring when K % 512 == 0: 65-128 rows 2-6% faster than two per CU with a 2-step ring); a
+//    workgroup's first and last segments may cover part of a tile and leave fp32 partial tiles,
+//    which gemm_sk_reduce_kernel adds in K order (the same bits whichever workgroup ran a segment).
 //  * Long K (>= 8192) with whole 256 x 256 tiles for at most 70% of the CUs and at least 256 rows
 //    (512-2048 rows of the down projection): the same stream-K over 256 x 256 tiles, one workgroup per CU.
 // The output tile is staged through LDS and stored as 16-byte row chunks.
@@ -806,6 +806,21 @@ int sk_occupancy(bool sb8) {
   return o;
 }
 
+// Resident workgroups per CU of the stream-K launch over 128 x 256 tiles (one: 205 VGPRs).
+int sk_wide_occupancy() {
+  static int o = 0;
+  if (o == 0) {
+    const void* f = reinterpret_cast<const void*>(&gemm_kernel<128, 256, true, kSkRing>);
+    constexpr size_t smem = GemmCfg<128, 256>::kSmem;
+    int nb = 0;
+    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kThreads, smem) != hipSuccess || nb < 1)
+      nb = 1;
+    o = nb < 2 ? nb : 2;
+  }
+  return o;
+}
+
 bool scale_rows_16b(const uint16_t* s, const uint16_t* b, int K) {
   return K % 512 == 0 && (reinterpret_cast<uintptr_t>(s) % 16) == 0 && (reinterpret_cast<uintptr_t>(b) % 16) == 0;
 }
@@ -831,6 +846,7 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   const int c = cus > 0 ? cus : 1;
   plan->sk = false;
   plan->sk256 = false;
+  plan->sk_wide = false;
   plan->tail_sk = false;
   plan->G = 0;
   plan->part_bytes = 0;
@@ -886,14 +902,25 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
     return true;
   }
   const bool sb8 = scale_rows_16b(s, b, K);
+  // 128 x 256 tiles (a step's fragment reads and barrier shared by twice the MFMAs, but partial
+  // tiles twice as large) past 128 rows or for K >= 8192; 128 x 128 below. A/B (interleaved rounds,
+  // within the parity tolerance): 256 / 384 / 160 x 5120 -> 17408 75.2 / 107.8 / 71.3 -> 74.0 /
+  // 94.4 / 69.5 us, 128 / 256 x 17408 -> 5120 51.1 / 82.2 -> 50.0 / 73.3 us, 200 x 5120 -> 10240
+  // 52.5 -> 50.1 us; at 113 / 128 x 5120 -> 17408 48.9 / 50.0 -> 51.4 / 51.9 us. Those splits
+  // give every workgroup at least 2.6 units; the wide tiles need at least 2 per CU.
   const int ups = sb8 ? 8 : 2;
-  const long long U = tiles * (K / BK / ups);
-  long long G = (long long)c * sk_occupancy(sb8);
+  const long long tiles_w = (long long)((M + 127) / 128) * ((N + 255) / 256);
+  const bool wide = sb8 && (M > 128 || K >= 8192) && tiles_w * (K / BK / ups) >= 2LL * c;
+  const long long tiles_sk = wide ? tiles_w : tiles;
+  const long long U = tiles_sk * (K / BK / ups);
+  long long G = (long long)c * (wide ? sk_wide_occupancy() : sk_occupancy(sb8));
   if (G > U) G = U;
-  const size_t slot = (size_t)GemmCfg<128, 128>::kPartF4 * 16 * 2;  // two partial tiles per workgroup
+  // two partial tiles per workgroup
+  const size_t slot = (size_t)(wide ? GemmCfg<128, 256>::kPartF4 : GemmCfg<128, 128>::kPartF4) * 16 * 2;
   if ((size_t)G * slot > ws_capacity) G = (long long)(ws_capacity / slot);
   if (G < 1 || G < c / 2) return true;  // too little workspace to spread the tiles: whole tiles instead
   plan->sk = true;
+  plan->sk_wide = wide;
   plan->G = (int)G;
   plan->part_bytes = (size_t)G * slot;
   return true;
@@ -923,8 +950,9 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
     return launch_sk_reduce<256, 256>(P, plan.G, stream);
   }
   if (plan.sk) {
+    if (plan.sk_wide && !sb8) return hipErrorInvalidValue;
     P.tiles_m = (M + 127) / 128;
-    P.tiles_n = (N + 127) / 128;
+    P.tiles_n = plan.sk_wide ? (N + 255) / 256 : (N + 127) / 128;
     P.tile0 = 0;
     P.quarter = 0;
     P.sk = 1;
@@ -932,6 +960,11 @@ hipError_t launch_gemm(const GemmPlan& plan, const uint16_t* x, const uint32_t* 
     P.upt = K / BK / P.ups;
     P.sk_tiles = P.tiles_m * P.tiles_n;
     P.U = (long long)P.sk_tiles * P.upt;
+    if (plan.sk_wide) {
+      hipError_t e = launch_tiles<128, 256, true, kSkRing>(P, plan.G, stream);
+      if (e != hipSuccess) return e;
+      return launch_sk_reduce<128, 256>(P, plan.G, stream);
+    }
     hipError_t e = sb8 ? launch_tiles<128, 128, true, kSkRing>(P, plan.G, stream)
                        : launch_tiles<128, 128, false>(P, plan.G, stream);
     if (e != hipSuccess) return e;

@@ -138,7 +138,8 @@ hipError_t launch_zero_u32(uint32_t* p, size_t n, hipStream_t stream);
 // (fp32 partials of split tiles in the workspace, added by a fix-up kernel behind the first).
 struct GemmPlan {
   bool sk;            // stream-K
-  bool sk256;         // stream-K over 256 x 256 tiles (else 128 x 128)
+  bool sk256;         // stream-K over 256 x 256 tiles (else 128 x 128, or 128 x 256 with sk_wide)
+  bool sk_wide;       // stream-K over 128 x 256 tiles
   bool tail_sk;       // whole tiles whose quarter-tile tail runs as stream-K over the quarters
   int G;              // stream-K workgroups (of the whole launch, or of the tail)
   size_t part_bytes;  // stream-K partial tiles (two per workgroup)

@@ -150,13 +150,15 @@ void check_gemm(int M, int N, int K, int cus) {
     const char* f = "gemm M=%d N=%d K=%d cus=%d cap=%zu";
 #define GP(cond) CHECK(cond, f, M, N, K, cus, cap)
     if (p.sk) {
-      const int t = p.sk256 ? 256 : 128;
-      const long long tiles = (long long)((M + t - 1) / t) * ((N + t - 1) / t);
+      const int tm = p.sk256 ? 256 : 128, tn = p.sk256 || p.sk_wide ? 256 : 128;
+      const long long tiles = (long long)((M + tm - 1) / tm) * ((N + tn - 1) / tn);
       const long long units = tiles * (K / 64 / (K % 512 == 0 ? 8 : 2));
       GP(p.G >= 1 && p.G <= units);
-      GP(p.part_bytes == (size_t)p.G * t * t * 4 * 2);
+      GP(p.part_bytes == (size_t)p.G * tm * tn * 4 * 2);
       GP(p.part_bytes <= cap);
+      GP(!(p.sk256 && p.sk_wide));
       if (p.sk256) GP(K % 512 == 0 && M >= 256 && p.G == cus);  // 8-step units, one workgroup per CU
+      if (p.sk_wide) GP(K % 512 == 0 && p.G <= cus);           // 8-step units, one workgroup per CU
     } else if (p.tail_sk) {
       // Whole tiles whose last round (fewer quarters than CUs) runs as stream-K over its quarters.
       const long long total = (long long)((M + 255) / 256) * ((N + 255) / 256);
@@ -165,7 +167,7 @@ void check_gemm(int M, int N, int K, int cus) {
       GP(p.G >= 1 && p.G <= 4 * rem * (K / 512));
       GP(p.part_bytes == (size_t)p.G * 128 * 128 * 4 * 2 && p.part_bytes <= cap);
     } else {
-      GP(!p.sk256 && p.part_bytes == 0);
+      GP(!p.sk256 && !p.sk_wide && p.part_bytes == 0);
     }
 #undef GP
   }
@@ -208,7 +210,8 @@ int query() {
         std::printf("none\n");
         continue;
       }
-      std::printf("sk=%d sk256=%d tail_sk=%d G=%d\n", (int)p.sk, (int)p.sk256, (int)p.tail_sk, p.G);
+      std::printf("sk=%d sk256=%d sk_wide=%d tail_sk=%d G=%d\n", (int)p.sk, (int)p.sk256, (int)p.sk_wide,
+                  (int)p.tail_sk, p.G);
     } else {
       std::printf("unknown\n");
     }

@@ -239,7 +239,9 @@ def workload_ref(x, w, s, b):
 # units of two K steps), the up projection at 128 rows, K = 1152 and K = 640, N = 784 and M = 200
 # (partial column and row tiles).
 # Also where whole 256 x 256 tiles would fill under half the CUs: 256 and 320 rows of the up
-# projection (272 and 408 tiles of 128). Long K with fewer whole 256 x 256 tiles than CUs takes
+# projection (272 and 408 tiles of 128), on 128 x 256 tiles, as are 120 x 17408 -> 5120 (K >= 8192)
+# and 136 x 5120 -> 10256 (partial row and column tiles; route_cases.GEMM_STREAM_K_CASES labels the
+# tile size of each). Long K with fewer whole 256 x 256 tiles than CUs takes
 # stream-K over those: 512 and 1024 rows of the down projection (40 and 80 tiles), 384 x 12288 ->
 # 5120 (a half-empty last row tile), 1000 x 8192 -> 4112 (partial row and column tiles). Whole
 # tiles whose last round has fewer quarters than CUs run it as stream-K over the quarters: 1024 x
@@ -248,7 +250,8 @@ def workload_ref(x, w, s, b):
 @pytest.mark.parametrize("m,k,n", [(65, 17536, 5120), (128, 5120, 17408), (100, 1152, 4096), (200, 5120, 784),
                                    (96, 640, 1024), (256, 5120, 17408), (320, 5120, 17408),
                                    (1024, 17408, 5120), (512, 17408, 5120), (384, 12288, 5120),
-                                   (1000, 8192, 4112), (1024, 5120, 17408), (4096, 1024, 1040)])
+                                   (1000, 8192, 4112), (1024, 5120, 17408), (4096, 1024, 1040),
+                                   (120, 17408, 5120), (136, 5120, 10256)])
 def test_gemm_stream_k_shapes(m, k, n):
     note(f"stream-K {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=m * 19 + k + n)
@@ -278,11 +281,12 @@ def test_gemm_stream_k_unaligned_scales():
 # One-hot rows through each form of the GEMM with 8-group scale blocks (K % 512 == 0): stream-K with
 # tiles split between workgroups (128 rows), 128 x 128 quarter tiles (1024 rows), whole 256 x 256
 # tiles (2048 rows, where x is the identity), stream-K over 256 x 256 tiles (512 rows, K = 8192),
+# stream-K over 128 x 256 tiles (256 x 4096 -> 8192),
 # stream-K over the quarters of a last round with fewer quarters than CUs (512 x 4096: 32 tiles,
 # all in that round; 2048 x 8448: 264 tiles, 256 whole and 8 cut into quarters). Each output is one dequantized weight, so every K
 # step's scale and bias group, in the fast and the general form, is checked bit for bit.
 @pytest.mark.parametrize("m,n,k", [(128, 4096, 2048), (1024, 8192, 2048), (2048, 8192, 2048), (512, 8192, 8192),
-                                   (512, 4096, 2048), (2048, 8448, 2048)])
+                                   (512, 4096, 2048), (2048, 8448, 2048), (256, 8192, 4096)])
 @pytest.mark.parametrize("kind", ["fast", "mixed", "slow"])
 def test_gemm_one_hot_is_exact_dequant(kind, m, n, k):
     note(f"GEMM one-hot {kind} {m}x{k}x{n}")

@@ -166,3 +166,13 @@ def test_rowphase_test_shapes_reach_the_rowphase_kernel(planner_exe):
              + [(m, n, k) for m, k, n in ROWPHASE_WINDOW_CASES] + [(m, n, k) for m, n, k, _ in ROWPHASE_WIDE_CASES])
     for case, route in zip(cases, dispatch_route(planner_exe, cases)):
         assert route == "row-phase", (case, route)
+
+
+def test_gemm_stream_k_cases_take_their_tiles(planner_exe):
+    """Each GEMM stream-K shape of test_gpu_parity.py runs on the tile size its label names."""
+    from route_cases import CUS, GEMM_STREAM_K_CASES
+
+    lines = [f"gemm {m} {n} {k} {CUS}" for m, n, k, _ in GEMM_STREAM_K_CASES]
+    for (m, n, k, tiles), p in zip(GEMM_STREAM_K_CASES, query(planner_exe, lines)):
+        assert p["sk"] == "1" and p["sk256"] == "0", (m, n, k, p)
+        assert p["sk_wide"] == ("1" if tiles == "128x256" else "0"), (m, n, k, tiles, p)
