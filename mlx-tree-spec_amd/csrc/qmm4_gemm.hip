@@ -882,8 +882,15 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   // tiles); 1536 x 17408 -> 5120 (120 full whole tiles, 480 quarters) 316 us, 419 on stream-K;
   // 512 and 1024 x 5120 -> 17408 (136 and 272 full tiles) stay on whole tiles.
   const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
-  const bool sk = tiles <= c || (2 * tiles256 < c && 4 * tiles <= 5LL * c) ||
-                  (M % 256 != 0 && tiles256 < c && tiles <= 2LL * c);
+  const bool sk_tiles = tiles <= c || (2 * tiles256 < c && 4 * tiles <= 5LL * c) ||
+                        (M % 256 != 0 && tiles256 < c && tiles <= 2LL * c);
+  // At most 128 rows over many columns: whole 256 x 256 tiles would pad the rows to 256, so
+  // stream-K over 128 x 256 tiles instead when that gives every CU at least 3 units. A/B against
+  // whole tiles (interleaved rounds, within the parity tolerance): 72 / 96 / 128 x 5120 -> 65984
+  // 141.5 / 144.3 / 148.0 -> 116.2 / 119.7 / 124.6 us, 128 x 5120 -> 248320 523.0 -> 405.9 us.
+  const bool sk_rows = !sk_tiles && M <= 128 && scale_rows_16b(s, b, K) &&
+                       (long long)((N + 255) / 256) * (K / 512) >= 3LL * c;
+  const bool sk = sk_tiles || sk_rows;
   if (!sk) {
     // A tail of fewer quarters than CUs: stream-K over the quarters (their K spread over every
     // CU) instead of one quarter per workgroup on a few CUs.
@@ -903,14 +910,15 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   }
   const bool sb8 = scale_rows_16b(s, b, K);
   // 128 x 256 tiles (a step's fragment reads and barrier shared by twice the MFMAs, but partial
-  // tiles twice as large) past 128 rows or for K >= 8192; 128 x 128 below. A/B (interleaved rounds,
+  // tiles twice as large) past 128 rows, for K >= 8192, or where stream-K replaces whole tiles at up
+  // to 128 rows (sk_rows); 128 x 128 otherwise. A/B (interleaved rounds,
   // within the parity tolerance): 256 / 384 / 160 x 5120 -> 17408 75.2 / 107.8 / 71.3 -> 74.0 /
   // 94.4 / 69.5 us, 128 / 256 x 17408 -> 5120 51.1 / 82.2 -> 50.0 / 73.3 us, 200 x 5120 -> 10240
   // 52.5 -> 50.1 us; at 113 / 128 x 5120 -> 17408 48.9 / 50.0 -> 51.4 / 51.9 us. Those splits
   // give every workgroup at least 2.6 units; the wide tiles need at least 2 per CU.
   const int ups = sb8 ? 8 : 2;
   const long long tiles_w = (long long)((M + 127) / 128) * ((N + 255) / 256);
-  const bool wide = sb8 && (M > 128 || K >= 8192) && tiles_w * (K / BK / ups) >= 2LL * c;
+  const bool wide = sb8 && (M > 128 || K >= 8192 || sk_rows) && tiles_w * (K / BK / ups) >= 2LL * c;
   const long long tiles_sk = wide ? tiles_w : tiles;
   const long long U = tiles_sk * (K / BK / ups);
   long long G = (long long)c * (wide ? sk_wide_occupancy() : sk_occupancy(sb8));

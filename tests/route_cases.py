@@ -110,8 +110,9 @@ ROWPHASE_ONE_HOT = [(32800, 32, 2048), (2064, 48, 2048), (65984, 16, 5120), (131
 ROWPHASE_WINDOW_CASES = [(12, 5120, 65552), (48, 3072, 33024), (64, 17408, 5120), (32, 5120, 65552),
                          (96, 17408, 5120)]
 
-# (M, N, K, tiles) of GEMM stream-K launches in test_gpu_parity.py: "128x256" tiles past 128 rows
-# or for K >= 8192 with 8-group scale blocks and at least 2 units per CU, else "128x128".
+# (M, N, K, tiles) of GEMM stream-K launches in test_gpu_parity.py: "128x256" tiles past 128 rows,
+# for K >= 8192, or at most 128 rows over enough columns that whole 256 x 256 tiles would otherwise
+# run (8-group scale blocks and at least 2 units per CU), else "128x128".
 GEMM_STREAM_K_CASES = [
     (128, 17408, 5120, "128x128"),   # the up projection at 128 rows
     (200, 784, 5120, "128x128"),     # too few units for the wide tiles
@@ -120,4 +121,6 @@ GEMM_STREAM_K_CASES = [
     (120, 5120, 17408, "128x256"),   # K >= 8192 at 120 rows
     (136, 10256, 5120, "128x256"),   # partial row and column tiles
     (256, 8192, 4096, "128x256"),    # the one-hot exact-dequant case
+    (72, 65984, 2048, "128x256"),    # at most 128 rows over many columns: instead of whole tiles
+    (96, 65984, 5120, "128x256"),
 ]

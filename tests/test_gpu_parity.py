@@ -240,8 +240,9 @@ def workload_ref(x, w, s, b):
 # (partial column and row tiles).
 # Also where whole 256 x 256 tiles would fill under half the CUs: 256 and 320 rows of the up
 # projection (272 and 408 tiles of 128), on 128 x 256 tiles, as are 120 x 17408 -> 5120 (K >= 8192)
-# and 136 x 5120 -> 10256 (partial row and column tiles; route_cases.GEMM_STREAM_K_CASES labels the
-# tile size of each). Long K with fewer whole 256 x 256 tiles than CUs takes
+# and 136 x 5120 -> 10256 (partial row and column tiles), and 72 / 96 rows over the 65984-column
+# head, where whole tiles would pad the rows to 256 (route_cases.GEMM_STREAM_K_CASES labels the tile
+# size of each). Long K with fewer whole 256 x 256 tiles than CUs takes
 # stream-K over those: 512 and 1024 rows of the down projection (40 and 80 tiles), 384 x 12288 ->
 # 5120 (a half-empty last row tile), 1000 x 8192 -> 4112 (partial row and column tiles). Whole
 # tiles whose last round has fewer quarters than CUs run it as stream-K over the quarters: 1024 x
@@ -251,7 +252,7 @@ def workload_ref(x, w, s, b):
                                    (96, 640, 1024), (256, 5120, 17408), (320, 5120, 17408),
                                    (1024, 17408, 5120), (512, 17408, 5120), (384, 12288, 5120),
                                    (1000, 8192, 4112), (1024, 5120, 17408), (4096, 1024, 1040),
-                                   (120, 17408, 5120), (136, 5120, 10256)])
+                                   (120, 17408, 5120), (136, 5120, 10256), (72, 2048, 65984), (96, 5120, 65984)])
 def test_gemm_stream_k_shapes(m, k, n):
     note(f"stream-K {m}x{k}x{n}")
     x, w, s, b = O.make_inputs(m, k, n, sigma=0.5, seed=m * 19 + k + n)
