@@ -3,7 +3,7 @@
 // Same arithmetic and operand layout as the skinny kernel (qmm4_skinny.hip; replaces the
 // reference's qmv_packed and 8-row NAX kernels for decode and small verify batches,
 // src/mlx_tree_spec/qmm_packed.py:151-220, 428-557), with a decomposition for the case where the
-// output columns alone fill the GPU: workgroup p (one per CU, 16 waves) owns the R consecutive
+// output columns alone fill the GPU: workgroup p (one per CU, 8 waves) owns the R consecutive
 // weight rows [p R, p R + R) over the whole of K, so workgroups share nothing and no partial sums
 // leave a CU.
 //
@@ -35,7 +35,7 @@
 //    each wave's two unit sums in registers until x is dead; the slots then take the x area.
 //  * Whole K over a large N whose slots do not fit (vocabulary heads): PAIR takes units in groups
 //    of consecutive steps of one block, one slot per group (pairs at 1-4 rows, groups of 5 at 5-8);
-//    OWN (9-16 rows, x alone filling up to all of LDS) gives wave w blocks w, w + 16, ... whole,
+//    OWN (9-16 rows, x alone filling up to all of LDS) gives wave w blocks w, w + 8, ... whole,
 //    their sums kept in registers and stored to y as each block's last step is done.
 //  * Fused gate+up (FUSED): w is [w_gate; w_up] (N rows, up rows from N / 2), y is [M, N / 2] =
 //    silu(x @ w_gate^T) * (x @ w_up^T). Workgroup p owns output columns [p R, p R + R); its 2R
@@ -53,7 +53,12 @@ namespace qmm4 {
 
 namespace {
 
-constexpr int kRsWaves = 16;
+// Two waves per SIMD: with 16 (four per SIMD) every CU kept twice the units in flight, and the
+// memory system served the decode shapes more slowly (A/B, interleaved rounds, identical bits:
+// c1 at M = 1 / 2 / 4 26.40 / 26.62 / 27.10 -> 25.96 / 25.96 / 27.16 us, 5120 -> 17408 / 10240 /
+// 12288 / 6144 / 1024 at 1-4 rows 5-9% faster, 9-16 rows over 17408 and 34816 2.5% faster; 16
+// rows over the 248320-column head 1.5% slower).
+constexpr int kRsWaves = 8;
 constexpr int kRsThreads = 64 * kRsWaves;
 // MP: x rows held per A fragment (4, 8 or 16; M <= MP). The MFMA's 16 rows are x rows
 // min(row, M - 1); output rows 4 g + r lie in lane group g, so a unit's sums live in the MP / 4
@@ -61,13 +66,18 @@ constexpr int kRsThreads = 64 * kRsWaves;
 constexpr int kRsPF = 2;  // units in flight per wave
 constexpr int kRsXB = 4;  // x pieces per thread per staging batch
 // SMALL plans: each wave holds at most kRsPF units for the whole launch, and all of x (at most
-// kRsSmallXP 16-byte pieces per thread: the whole LDS) is loaded global -> LDS directly.
+// kRsSmallXP 16-byte pieces per thread, 80 KB) is loaded global -> LDS directly; OWN plans hold
+// at most as much x. (Allowing the whole LDS at 8 waves sent 9-16 rows over 65552-99984 columns
+// to OWN instead of the row-phase kernel, 3.5-4% slower; 5-8 rows over a small N run the SMALL
+// form 7% faster than with 16 waves either way.)
 constexpr int kRsSmallXP = 10;
 constexpr size_t kRsLds = 160 * 1024;
 // NORM: each row of x is normalised by one group of 256 threads, 16-byte chunks t, t + 256, ... of
-// the row per thread, at most kRsNormChunks each (K <= 8192).
+// the row per thread, at most kRsNormChunks each (K <= 8192); the workgroup's threads take the MP
+// rows kRsNormRows at a time (the add_rms_norm kernel's thread layout and summation order).
 constexpr int kRsNormThreads = 256;
 constexpr int kRsNormChunks = 4;
+constexpr int kRsNormRows = kRsThreads / kRsNormThreads;
 
 struct RowSplitParams {
   const uint16_t* x;
@@ -141,13 +151,13 @@ __host__ __device__ inline size_t rowsplit_red_offset(int Kp, int MP, int units,
 // stages its K slice of n, and workgroup 0 writes h and n.
 // PAIR: 0, or units taken in groups: 1 for pairs, 2 for groups of P.GU > 2.
 template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, int PAIR = 0, bool OWN = false>
-__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(4)))
+__global__ __launch_bounds__(kRsThreads) __attribute__((amdgpu_waves_per_eu(kRsWaves / 4)))
 void rowsplit_kernel(RowSplitParams P) {
   static_assert(MP == 4 || MP == 8 || MP == 16, "x rows per fragment");
   static_assert(!SMALL || (!FUSED && !KSPLIT && !NORM), "small plans are plain whole-K projections of 6+ rows");
   static_assert(!PAIR || (!FUSED && !KSPLIT && !SMALL && !NORM), "paired units are plain whole-K projections");
   static_assert(!OWN || (!FUSED && !KSPLIT && !SMALL && !NORM && !PAIR && V == 4), "own blocks: plain whole-K projections");
-  static_assert(!NORM || (MP == 4 && kRsThreads == MP * kRsNormThreads), "one thread group per normalised row");
+  static_assert(!NORM || (MP == 4 && MP % kRsNormRows == 0), "thread groups of 256 per normalised row");
   constexpr int G = MP / 4;  // lane groups holding output rows
   typedef f32x4 RowSums[G];  // the sums of one output column over x rows 4 g + r
   extern __shared__ __attribute__((aligned(16))) uint8_t lds[];
@@ -230,23 +240,32 @@ void rowsplit_kernel(RowSplitParams P) {
     }
     load_x(nxb - 1);
   }
-  // NORM: row grp of x and r, and the norm weight, for chunks c = tn + 256 i (rows >= M and chunks
-  // past the row read as zero).
-  const int grp = tid / kRsNormThreads, tn = tid - grp * kRsNormThreads;
-  u32x4 nx[kRsNormChunks], nr[kRsNormChunks], nwt[kRsNormChunks];
+  // NORM: in pass q, row q * kRsNormRows + tid / 256 of x and r, and the norm weight, for chunks
+  // c = tn + 256 i (rows >= M and chunks past the row read as zero).
+  constexpr int kNP = NORM ? MP / kRsNormRows : 1;  // row passes
+  const int grp0 = tid / kRsNormThreads, tn = tid - grp0 * kRsNormThreads;
+  u32x4 nx[kNP][kRsNormChunks], nr[kNP][kRsNormChunks], nwt[kRsNormChunks];
   if constexpr (NORM) {
     const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(P.r), 0, rsrc_bytes((unsigned long long)P.M * P.K * 2), kBufferRsrcWord3);
     const __amdgpu_buffer_rsrc_t rn = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<uint16_t*>(P.nw), 0, rsrc_bytes((unsigned long long)P.K * 2), kBufferRsrcWord3);
 #pragma unroll
+    for (int q = 0; q < kNP; ++q) {
+      const int grp = q * kRsNormRows + grp0;
+#pragma unroll
+      for (int i = 0; i < kRsNormChunks; ++i) {
+        const int c = tn + i * kRsNormThreads;
+        const bool live = grp < P.M && c < (P.K >> 3);
+        const uint32_t off = live ? ((uint32_t)grp * (uint32_t)P.K + (uint32_t)c * 8u) * 2u : 0x80000000u;
+        nx[q][i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
+        nr[q][i] = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0);
+      }
+    }
+#pragma unroll
     for (int i = 0; i < kRsNormChunks; ++i) {
       const int c = tn + i * kRsNormThreads;
-      const bool live = grp < P.M && c < (P.K >> 3);
-      const uint32_t off = live ? ((uint32_t)grp * (uint32_t)P.K + (uint32_t)c * 8u) * 2u : 0x80000000u;
-      nx[i] = __builtin_amdgcn_raw_buffer_load_b128(rx, off, 0, 0);
-      nr[i] = __builtin_amdgcn_raw_buffer_load_b128(rr, off, 0, 0);
-      nwt[i] = __builtin_amdgcn_raw_buffer_load_b128(rn, live ? (uint32_t)c * 16u : 0x80000000u, 0, 0);
+      nwt[i] = __builtin_amdgcn_raw_buffer_load_b128(rn, c < (P.K >> 3) ? (uint32_t)c * 16u : 0x80000000u, 0, 0);
     }
   }
   // Every wave's x loads enter the CU's memory pipeline before any weight fetch: the pipeline
@@ -310,32 +329,40 @@ void rowsplit_kernel(RowSplitParams P) {
   }
 
   if constexpr (NORM) {
-    // h and the row's sum of squares, then the row sums of the group's 4 waves in wave order.
+    // h and the row's sum of squares, then the row sums of its group's 4 waves in wave order
+    // (row grp's waves write red[4 grp .. 4 grp + 3]).
     float* red = reinterpret_cast<float*>(lds + rowsplit_red_offset(P.Kp, MP, U, SMALL));
-    float ss = 0.0f;
 #pragma unroll
-    for (int i = 0; i < kRsNormChunks; ++i) nx[i] = norm_add_chunk(nx[i], nr[i], ss);
-    ss = norm_wave_sum(ss);
-    if (lane == 0) red[wave] = ss;
+    for (int q = 0; q < kNP; ++q) {
+      float ss = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kRsNormChunks; ++i) nx[q][i] = norm_add_chunk(nx[q][i], nr[q][i], ss);
+      ss = norm_wave_sum(ss);
+      if (lane == 0) red[q * kRsWaves + wave] = ss;
+    }
     __syncthreads();
-    float total = 0.0f;
-#pragma unroll
-    for (int i = 0; i < kRsNormThreads / 64; ++i) total += red[grp * (kRsNormThreads / 64) + i];
-    const float inv = norm_inv(total, P.K, P.eps);
     // n into the x stage (this workgroup's K slice: pieces kq / 8 .. kq / 8 + S * 16 - 1), and h, n
     // to memory from workgroup 0.
     const bool first = blockIdx.x == 0;
 #pragma unroll
-    for (int i = 0; i < kRsNormChunks; ++i) {
-      const int c = tn + i * kRsNormThreads;
-      if (grp < P.M && c < (P.K >> 3)) {
-        const u32x4 nv = norm_scale_chunk(nx[i], nwt[i], inv);
-        const int sq = c - (kq >> 3);
-        if (sq >= 0 && sq < S * 16) xs[sq * MP + grp] = nv;
-        if (first) {
-          const size_t o = (size_t)grp * P.K + (size_t)c * 8;
-          *reinterpret_cast<u32x4*>(P.h_out + o) = nx[i];
-          *reinterpret_cast<u32x4*>(P.n_out + o) = nv;
+    for (int q = 0; q < kNP; ++q) {
+      const int grp = q * kRsNormRows + grp0;
+      float total = 0.0f;
+#pragma unroll
+      for (int i = 0; i < kRsNormThreads / 64; ++i) total += red[grp * (kRsNormThreads / 64) + i];
+      const float inv = norm_inv(total, P.K, P.eps);
+#pragma unroll
+      for (int i = 0; i < kRsNormChunks; ++i) {
+        const int c = tn + i * kRsNormThreads;
+        if (grp < P.M && c < (P.K >> 3)) {
+          const u32x4 nv = norm_scale_chunk(nx[q][i], nwt[i], inv);
+          const int sq = c - (kq >> 3);
+          if (sq >= 0 && sq < S * 16) xs[sq * MP + grp] = nv;
+          if (first) {
+            const size_t o = (size_t)grp * P.K + (size_t)c * 8;
+            *reinterpret_cast<u32x4*>(P.h_out + o) = nx[q][i];
+            *reinterpret_cast<u32x4*>(P.n_out + o) = nv;
+          }
         }
       }
     }
@@ -951,7 +978,7 @@ bool rowsplit_plan(int M, int N, int K, int cus, bool fused, RowSplitPlan* plan)
 size_t rowsplit_smem(const RowSplitPlan& plan, bool norm) {
   if (!norm) return plan.smem;
   return std::max(plan.smem, rowsplit_red_offset(plan.Kp, plan.MP, plan.RB * plan.SU, plan.small) +
-                                 sizeof(float) * (kRsThreads / 64));
+                                 sizeof(float) * plan.MP * (kRsNormThreads / 64));
 }
 
 template <int MP, int V, bool FUSED, bool KSPLIT, bool SMALL, bool NORM, int PAIR = 0, bool OWN = false>

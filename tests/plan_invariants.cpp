@@ -38,6 +38,10 @@ long long g_fail = 0, g_checked = 0;
 size_t xs_bytes(int kp, int mp) { return (size_t)(kp >> 7) * 16 * mp * 16; }
 size_t part_bytes(int units, int mp) { return (size_t)units * (mp / 4) * 16 * 16; }
 
+// Waves of a row-split workgroup (kRsWaves in qmm4_rowsplit.hip) and units in flight per wave.
+constexpr int kRowSplitWaves = 8;
+constexpr int kRowSplitRing = 2;
+
 void check_rowsplit(int M, int N, int K, int cus, bool fused) {
   RowSplitPlan p{};
   if (!rowsplit_plan(M, N, K, cus, fused, &p)) return;
@@ -67,7 +71,7 @@ void check_rowsplit(int M, int N, int K, int cus, bool fused) {
   RS(modes <= 1);
   if (p.small) {
     RS(p.KS == 1 && p.V == 4 && !fused);
-    RS(p.RB * p.SU <= 32);  // every unit in the 16 waves' two-slot rings at once
+    RS(p.RB * p.SU <= kRowSplitWaves * kRowSplitRing);  // every unit in the waves' rings at once
   }
   if (p.pair) {
     // Launched only as whole-K, unfused, 4-step units; the groups tile each block's steps.
@@ -78,7 +82,7 @@ void check_rowsplit(int M, int N, int K, int cus, bool fused) {
   if (p.own) {
     // Launched only as whole-K, unfused, 4-step units; every wave owns at least two blocks.
     RS(p.KS == 1 && p.V == 4 && !fused);
-    RS(p.RB >= 32);
+    RS(p.RB >= 2 * kRowSplitWaves);
     RS(p.smem == xs_bytes(p.Kp, p.MP));
   }
   if (!p.small && !p.pair && !p.own)
