@@ -789,35 +789,31 @@ hipError_t launch_sk_reduce(const GemmParams& P, int G, hipStream_t stream) {
   return hipGetLastError();
 }
 
+// Resident workgroups per CU of a kernel with `smem` bytes of dynamic LDS (at most 2, at least 1).
+int resident_per_cu(const void* f, size_t smem) {
+  int nb = 0;
+  if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess ||
+      hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kThreads, smem) != hipSuccess || nb < 1)
+    nb = 1;
+  return nb < 2 ? nb : 2;
+}
+
 // Resident stream-K workgroups per CU (the 128 x 128 configuration: 74 KB of LDS each).
 int sk_occupancy(bool sb8) {
   static int occ[2] = {0, 0};
   int& o = occ[sb8 ? 1 : 0];
-  if (o == 0) {
-    const void* f = sb8 ? reinterpret_cast<const void*>(&gemm_kernel<128, 128, true, kSkRing>)
-                        : reinterpret_cast<const void*>(&gemm_kernel<128, 128, false>);
-    constexpr size_t smem = GemmCfg<128, 128>::kSmem;
-    int nb = 0;
-    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kThreads, smem) != hipSuccess || nb < 1)
-      nb = 1;
-    o = nb < 2 ? nb : 2;
-  }
+  if (o == 0)
+    o = resident_per_cu(sb8 ? reinterpret_cast<const void*>(&gemm_kernel<128, 128, true, kSkRing>)
+                            : reinterpret_cast<const void*>(&gemm_kernel<128, 128, false>),
+                        GemmCfg<128, 128>::kSmem);
   return o;
 }
 
 // Resident workgroups per CU of the stream-K launch over 128 x 256 tiles (one: 205 VGPRs).
 int sk_wide_occupancy() {
   static int o = 0;
-  if (o == 0) {
-    const void* f = reinterpret_cast<const void*>(&gemm_kernel<128, 256, true, kSkRing>);
-    constexpr size_t smem = GemmCfg<128, 256>::kSmem;
-    int nb = 0;
-    if (hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)smem) != hipSuccess ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&nb, f, kThreads, smem) != hipSuccess || nb < 1)
-      nb = 1;
-    o = nb < 2 ? nb : 2;
-  }
+  if (o == 0)
+    o = resident_per_cu(reinterpret_cast<const void*>(&gemm_kernel<128, 256, true, kSkRing>), GemmCfg<128, 256>::kSmem);
   return o;
 }
 
