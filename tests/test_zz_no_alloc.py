@@ -150,7 +150,8 @@ def test_noalloc_captures_where_the_allocating_entry_cannot():
 # slices (counters + partials), row-phase with a K split (partials), K-split verify (counters +
 # partials), stream-K skinny (counters + partials); the GEMM's stream-K over 128 x 128 tiles on a
 # few and on 256 workgroups (32 MiB of partials); its stream-K over 256 x 256 tiles (128 MiB of
-# partials, the largest workspace) and over the quarters of a last round of whole tiles.
+# partials, the largest workspace), over the quarters of a last round of whole tiles, and over
+# 128 x 256 tiles (64 MiB of partials).
 PAIRS = [
     ((2, 5120, 17408), (1, 2048, 8192)),
     ((64, 5120, 17408), (24, 2048, 5120)),
@@ -159,6 +160,7 @@ PAIRS = [
     ((96, 640, 1024), (80, 256, 512)),
     ((512, 5120, 17408), (128, 17408, 5120)),
     ((1024, 17408, 5120), (96, 512, 1024)),
+    ((256, 17408, 5120), (136, 10256, 5120)),  # stream-K over 128 x 256 tiles, then a partial one
 ]
 
 
