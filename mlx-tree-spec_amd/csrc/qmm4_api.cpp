@@ -299,6 +299,28 @@ int check_qmm_args(const void* x, const uint32_t* w, const void* scales, const v
   return QMM4_OK;
 }
 
+// Past 64 rows the row-phase kernel takes up to kRowPhaseMaxM rows over a small N (its weights are
+// dequantized once for all rows), and up to kRowPhaseMaxMNarrow when N is at most
+// kRowPhaseNarrowN (the GEMM then has too few 128 x 128 tiles). Measured against the GEMM (A/B,
+// interleaved rounds, the model's up and down projections): 65 / 80 / 96 / 112 rows 38.5 / 40.2 /
+// 44.2 / 47.4 us against 46.7 / 47.2 / 48.5 / 48.6 us (5120 -> 17408), 35.8 / 36.7 / 40.4 / 44.2
+// against 45.5 / 46.5 / 47.8 / 48.8 (17408 -> 5120); at 120-128 rows (one block per wave) 53-74
+// against 48-51 us, but 128 x 5120 -> 1024 17.3 against 47.6 us. A wide plan (every workgroup its
+// own blocks over all of K) is taken up to kRowPhaseMaxMWide rows when it needs at most one range
+// per CU: 65 / 80 / 96 x 5120 -> 34816 57.5 / 64.5 / 71.9 us against 71.8 / 73.3 / 73.5 us on the
+// GEMM, 72 x 4096 -> 32768 43.6 against 50.1 us; at 112 rows 80.8 against 74.5 us.
+constexpr int kRowPhaseMaxM = 112;
+constexpr int kRowPhaseMaxMWide = 96;
+constexpr int kRowPhaseMaxMNarrow = 128;
+constexpr int kRowPhaseNarrowN = 2048;
+// The fused gate+up row-phase plan's ranges hold whole blocks of both halves, so they may hold one
+// block more than the projection's (N = 34816 on 256 CUs: 218 ranges of 10 against 242 of 9). From
+// 17 rows and up to this M x K the saved epilogue pass outweighs that block (A/B, N = 34816):
+// 24 x 16384 102.7 against 106.1 us, 48 x 10240 90.0 / 91.8, 96 x 5120 73.3 / 74.5; past it
+// 80 x 8192 94.6 / 94.0, 64 x 16384 153.9 / 153.3; and 12 x 20480 113.5 / 108.1 (12 rows draw more
+// of their time from HBM, where the 24 idle CUs count).
+constexpr long long kFusedRowPhaseMaxMK = 1LL << 19;
+
 int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, const void* scales,
                           const void* biases, void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream,
                           WorkspaceSource& ws) {
@@ -321,6 +343,23 @@ int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, cons
     if (e != hipSuccess) return hip_error(e, "fused gate+up row-split kernel launch");
     return QMM4_OK;
   }
+  // Rows the projection would give a wide row-phase plan (not the row-split kernel, up to 16 rows):
+  // that plan with the epilogue fused, each range holding the same blocks of the gate and up
+  // halves. Against the projection and the epilogue pass (A/B, 5120 -> 34816): 24 / 32 / 48 / 64 /
+  // 80 / 96 rows 40.8 / 42.6 / 52.6 / 59.0 / 66.8 / 73.3 us against 42.6 / 44.0 / 54.2 / 60.6 /
+  // 67.7 / 74.5 us, the same bits; 24 x 16384 -> 32768 (ranges of 8 blocks in both) 84.9 against
+  // 89.1 us.
+  if (M >= 5 && M <= kRowPhaseMaxMWide && aligned(scales, 16) && aligned(biases, 16) && K % 512 == 0 &&
+      !(M <= 16 && rowsplit_plan((int)M, (int)N, (int)K, di->cus, false, &rplan))) {
+    RowPhasePlan pplan, uplan;
+    if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan, true) && (M <= 64 || pplan.ranges <= di->cus) &&
+        rowphase_plan((int)M, (int)N, (int)K, di->cus, &uplan) &&
+        (pplan.BW <= uplan.BW || (M >= 17 && M * K <= kFusedRowPhaseMaxMK))) {
+      e = launch_rowphase(pplan, xb, w, sb, bb, yb, nullptr, (int)M, (int)N, (int)K, stream);
+      if (e != hipSuccess) return hip_error(e, "fused gate+up row-phase kernel launch");
+      return QMM4_OK;
+    }
+  }
   // Otherwise the projection into a library-held [M, N] buffer, then the epilogue as its own pass.
   void* t = nullptr;
   rc = ws.get_scratch((size_t)M * (size_t)N * sizeof(uint16_t), &t);
@@ -332,22 +371,8 @@ int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, cons
   return QMM4_OK;
 }
 
-// The kernel choice for y = x @ dequant(w)^T (arguments already checked, M and N > 0, api_mutex held).
-// Past 64 rows the row-phase kernel takes up to kRowPhaseMaxM rows over a small N (its weights are
-// dequantized once for all rows), and up to kRowPhaseMaxMNarrow when N is at most
-// kRowPhaseNarrowN (the GEMM then has too few 128 x 128 tiles). Measured against the GEMM (A/B,
-// interleaved rounds, the model's up and down projections): 65 / 80 / 96 / 112 rows 38.5 / 40.2 /
-// 44.2 / 47.4 us against 46.7 / 47.2 / 48.5 / 48.6 us (5120 -> 17408), 35.8 / 36.7 / 40.4 / 44.2
-// against 45.5 / 46.5 / 47.8 / 48.8 (17408 -> 5120); at 120-128 rows (one block per wave) 53-74
-// against 48-51 us, but 128 x 5120 -> 1024 17.3 against 47.6 us. A wide plan (every workgroup its
-// own blocks over all of K) is taken up to kRowPhaseMaxMWide rows when it needs at most one range
-// per CU: 65 / 80 / 96 x 5120 -> 34816 57.5 / 64.5 / 71.9 us against 71.8 / 73.3 / 73.5 us on the
-// GEMM, 72 x 4096 -> 32768 43.6 against 50.1 us; at 112 rows 80.8 against 74.5 us.
-constexpr int kRowPhaseMaxM = 112;
-constexpr int kRowPhaseMaxMWide = 96;
-constexpr int kRowPhaseMaxMNarrow = 128;
-constexpr int kRowPhaseNarrowN = 2048;
 
+// The kernel choice for y = x @ dequant(w)^T (arguments already checked, M and N > 0, api_mutex held).
 int dispatch_qmm(DeviceInfo* di, const void* x, const uint32_t* w, const void* scales, const void* biases,
                  void* y, int64_t M, int64_t N, int64_t K, hipStream_t stream, WorkspaceSource& ws) {
   const uint16_t* xb = static_cast<const uint16_t*>(x);

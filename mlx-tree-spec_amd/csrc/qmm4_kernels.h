@@ -68,10 +68,11 @@ struct RowPhasePlan {
   size_t lds;         // dynamic LDS bytes
   size_t part_bytes;  // partial-tile workspace (S > 1)
   bool wide;          // every workgroup takes all of K (N fills the GPU)
+  bool fused;         // gate+up: w stacks [gate; up] (N = 2 n rows), y = silu(gate) * up is [M, n]
 };
-bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan);
+bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan, bool fused = false);
 // `part` holds plan.part_bytes (used when plan.S > 1: the partial tiles, added by a second kernel
-// launched behind the first on the same stream).
+// launched behind the first on the same stream). A fused plan writes y as [M, N / 2].
 hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const uint32_t* w, const uint16_t* s,
                            const uint16_t* b, uint16_t* y, float* part, int M, int N, int K, hipStream_t stream);
 

@@ -55,6 +55,7 @@ struct RowPhaseParams {
   int S;          // workgroups per range (K split)
   int NP;         // phases along K
   int ranges;     // block ranges
+  int fused;      // gate+up with the SiLU·mul epilogue (wide plans): w stacks [gate; up], y is [M, N / 2]
 };
 
 template <int MB_, int V_, int BPW_, int W_, int STG_ = 3, bool OPT_ = false>
@@ -70,6 +71,7 @@ struct RpCfg {
   // The last block slot's arithmetic runs only in the waves that hold a BPW-th block (wide plans
   // whose blocks leave some waves one short); otherwise every wave computes every slot.
   static constexpr bool kOptLast = OPT_ && BPW > 1;
+  static constexpr bool kFusable = MB_ <= 6;  // the fused gate+up epilogue is built (up to 96 rows)
   static constexpr int kXPieces = V * 16 * MP;    // 16-byte x pieces per phase
   static constexpr int kSB = 4 * V;               // bytes of scales (or biases) per row and phase
   static constexpr int WP = 64 / kSB;             // phases per scale window (64 bytes of each row)
@@ -115,8 +117,21 @@ void rowphase_kernel(RowPhaseParams P) {
   const int split = P.S > 1 ? q / P.ranges : 0;
   const int range = P.S > 1 ? q - split * P.ranges : q;
   const int p = range * P.S + split;  // the partial tile's slot (range-major: the reduce kernel's order)
+  // Fused gate+up: the range holds BW / 2 output blocks, gate blocks hb0 .. hb0 + hb - 1 (local
+  // blocks 0 .. hb - 1) and the same blocks of the up half (local hb .. 2 hb - 1).
+  // (Built for up to 96 rows: the fused planner takes no more.)
+  const bool fused = C::kFusable && P.fused;
+  const int NBh = P.NB >> 1;
+  const int hb0 = range * (P.BW >> 1);
+  const int hb = fused ? min(P.BW >> 1, NBh - hb0) : 0;
   const int b0 = range * P.BW;
-  const int nbr = min(P.BW, P.NB - b0);  // blocks in this range
+  const int nbr = fused ? 2 * hb : min(P.BW, P.NB - b0);  // blocks in this range
+  // Weight row of local row lr of the range.
+  auto grow = [&](int lr) __attribute__((always_inline)) {
+    const int lb = lr >> 4;
+    const int gb = !fused ? b0 + lb : lb < hb ? hb0 + lb : NBh + hb0 + (lb - hb);
+    return 16 * gb + (lr & 15);
+  };
   const int pa = (int)((long long)split * P.NP / P.S);
   const int pb = (int)((long long)(split + 1) * P.NP / P.S);
   const int np = pb - pa;
@@ -178,7 +193,7 @@ void rowphase_kernel(RowPhaseParams P) {
         const int i = tid + j * kRpThreads;
         const int row = i / kPR, pc = i - row * kPR;
         const bool ok = row < nrows && g0 + pc * 8 < KG;
-        const uint32_t off = ok ? (uint32_t)(r0 + row) * (uint32_t)KG * 2u + (uint32_t)(g0 + pc * 8) * 2u : kOut;
+        const uint32_t off = ok ? (uint32_t)grow(row) * (uint32_t)KG * 2u + (uint32_t)(g0 + pc * 8) * 2u : kOut;
         r[arr][j] = __builtin_amdgcn_raw_buffer_load_b128(arr == 0 ? rs : rb, off, 0, 0);
       }
   };
@@ -211,8 +226,7 @@ void rowphase_kernel(RowPhaseParams P) {
   uint32_t wo[BPW];
 #pragma unroll
   for (int j = 0; j < BPW; ++j) {
-    const int row = r0 + 16 * (wave + kRpWaves * j) + n;
-    wo[j] = (j < nbw) ? (uint32_t)row * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
+    wo[j] = (j < nbw) ? (uint32_t)grow(16 * (wave + kRpWaves * j) + n) * (uint32_t)(P.K >> 1) + (uint32_t)g * 16u : kOut;
   }
   // Piece v of every block of phase ph into register buffer J (a zero-length resource when the
   // phase does not exist: the loads then read zero without touching memory).
@@ -367,8 +381,9 @@ void rowphase_kernel(RowPhaseParams P) {
   if (i < np) phase(pa + i, std::integral_constant<int, 0>{});
 
   // ---- epilogue ----
+  const int ny = fused ? P.N >> 1 : P.N;  // columns of y
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
-      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * ny * 2), kBufferRsrcWord3);
   // bf16 tile of y through LDS: tile[m][local column], then 16-byte row chunks.
   uint16_t* yt = reinterpret_cast<uint16_t*>(lds);
   auto write_y = [&]() __attribute__((always_inline)) {
@@ -378,6 +393,21 @@ void rowphase_kernel(RowPhaseParams P) {
       const int m = c / cpr, q = c - m * cpr;
       const u32x4 v = *reinterpret_cast<const u32x4*>(yt + m * RW + q * 8);
       __builtin_amdgcn_raw_buffer_store_b128(v, ry, ((uint32_t)m * (uint32_t)P.N + (uint32_t)(r0 + q * 8)) * 2u, 0, 0);
+    }
+  };
+  // Fused: output columns 16 hb0 .. 16 (hb0 + hb) - 1 of y = silu(gate) * up, from the tile's gate
+  // (local columns below 16 hb) and up halves, bf16 values as the unfused projection writes them.
+  auto write_y_fused = [&]() __attribute__((always_inline)) {
+    const int cpr = hb * 2;  // 8-column chunks per row
+    for (int c = tid; c < P.M * cpr; c += kRpThreads) {
+      const int m = c / cpr, q = c - m * cpr;
+      const u32x4 gv = *reinterpret_cast<const u32x4*>(yt + m * RW + q * 8);
+      const u32x4 uv = *reinterpret_cast<const u32x4*>(yt + m * RW + hb * 16 + q * 8);
+      u32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        o[e] = silu_mul_bf16(gv[e] & 0xFFFFu, uv[e] & 0xFFFFu) | (silu_mul_bf16(gv[e] >> 16, uv[e] >> 16) << 16);
+      __builtin_amdgcn_raw_buffer_store_b128(o, ry, ((uint32_t)m * (uint32_t)ny + (uint32_t)(16 * hb0 + q * 8)) * 2u, 0, 0);
     }
   };
   auto tile_to_lds = [&](const f32x4 (&a)[BPW][MB]) __attribute__((always_inline)) {
@@ -404,7 +434,10 @@ void rowphase_kernel(RowPhaseParams P) {
     __syncthreads();
     tile_to_lds(acc);
     __syncthreads();
-    write_y();
+    if (fused)
+      write_y_fused();
+    else
+      write_y();
     return;
   }
 
@@ -547,8 +580,8 @@ static const void* rowphase_func(int id) {
 
 constexpr int kRpNarrowBpw = 2;  // blocks per wave when K is split
 
-bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
-  if (M < 1 || M > 128 || N % 16 != 0 || cus < 1) return false;
+bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan, bool fused) {
+  if (M < 1 || M > 128 || N % (fused ? 32 : 16) != 0 || cus < 1) return false;
   // Row blocks of x: 16, 32 or 64 rows, then 80 to 128 (variants with two x stages).
   const int mb = M <= 16 ? 1 : M <= 32 ? 2 : M <= 64 ? 4 : (M + 15) / 16;
   const int NB = N / 16;
@@ -559,6 +592,10 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   // kRpNarrowBpw blocks per wave, K split over the CUs.
   constexpr int kW = 8;  // waves per workgroup of every variant
   const bool wide = NB >= kW * cus;
+  // Fused gate+up (N = 2 n stacked rows): wide plans only, each range the same BW / 2 blocks of
+  // both halves, so that the SiLU·mul epilogue finds gate and up columns in one tile.
+  if (fused && (!wide || M > 96)) return false;
+  const int NBh = NB / 2;
   // The variant for mb rows with the fewest blocks per wave that still holds `want` (or the most).
   auto pick = [&](int want) {
     int id = -1, best_b = 0;
@@ -601,6 +638,7 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
     passes = (share + kW * maxb - 1) / (kW * maxb);
     bw = (NB + cus * passes - 1) / (cus * passes);
   }
+  if (fused) bw = 2 * ((NBh + cus * passes - 1) / (cus * passes));
   // Narrow: ranges of kRpNarrowBpw or one more block per wave, whichever gives a workgroup the
   // shorter walk (blocks x phases of its K slice x super-steps per phase) with the grid filling
   // the CUs; a tie keeps the smaller ranges (fewer partial tiles to add). 17-32 rows over
@@ -666,7 +704,7 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   const int NP = ks / v;
   int BW, S;
   if (wide) {
-    BW = bw < kW * bpw ? bw : kW * bpw;
+    BW = bw < kW * bpw ? bw : kW * bpw;  // even when fused: bw is, and so is kW * bpw
     S = 1;
   } else {
     BW = kW * bpw;
@@ -679,11 +717,12 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan) {
   plan->BW = BW;
   plan->S = S;
   plan->NP = NP;
-  plan->ranges = (NB + BW - 1) / BW;
+  plan->ranges = fused ? (NBh + BW / 2 - 1) / (BW / 2) : (NB + BW - 1) / BW;
   plan->blocks = plan->ranges * S;
   plan->lds = lds;
   plan->part_bytes = S > 1 ? (size_t)plan->blocks * items * 16 : 0;
   plan->wide = wide;
+  plan->fused = fused;
   return true;
 }
 
@@ -693,6 +732,14 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
   P.x = x; P.s = s; P.b = b; P.w = w; P.y = y; P.part = part;
   P.M = M; P.N = N; P.K = K;
   P.NB = N / 16; P.BW = plan.BW; P.S = plan.S; P.NP = plan.NP; P.ranges = plan.ranges;
+  P.fused = plan.fused ? 1 : 0;
+  if (plan.fused) {
+    int cm, cv, cb, items;
+    size_t l;
+    if (!rowphase_geometry(plan.variant, &cm, &cv, &cb, &l, &items) || cm > 6 || plan.S != 1 || plan.BW % 2 != 0 ||
+        N % 32 != 0)
+      return hipErrorInvalidValue;
+  }
   const void* f = rowphase_func(plan.variant);
   if (!f) return hipErrorInvalidValue;
   hipError_t e = hipFuncSetAttribute(f, hipFuncAttributeMaxDynamicSharedMemorySize, (int)plan.lds);

@@ -121,7 +121,20 @@ void check_rowphase(int M, int N, int K, int cus) {
   RP(p.lds <= kLds);
   RP((p.S > 1) == (p.part_bytes > 0));
   RP(!p.wide || p.S == 1);
+  RP(!p.fused);
 #undef RP
+  // Fused gate+up: a wide plan whose ranges hold the same BW / 2 blocks of both halves.
+  RowPhasePlan q{};
+  if (N % 32 != 0 || !rowphase_plan(M, N, K, cus, &q, true)) return;
+  ++g_checked;
+  const char* ff = "rowphase fused M=%d N=%d K=%d cus=%d";
+#define RF(cond) CHECK(cond, ff, M, N, K, cus)
+  const int nbh = N / 32;
+  RF(q.fused && q.wide && q.S == 1 && q.part_bytes == 0);
+  RF(q.BW >= 2 && q.BW % 2 == 0);
+  RF((long long)q.ranges * (q.BW / 2) >= nbh && (long long)(q.ranges - 1) * (q.BW / 2) < nbh);
+  RF(q.blocks == q.ranges && q.lds <= kLds && q.NP >= 1);
+#undef RF
 }
 
 void check_verify(int M, int N, int K, int cus) {
@@ -180,7 +193,7 @@ void check_gemm(int M, int N, int K, int cus) {
 }  // namespace
 
 // Query mode (`plan_invariants query`): one shape per stdin line, "<planner> M N K cus", with
-// planner rowsplit, rowsplit_fused, xreg, rowphase or gemm; prints one line per query with the
+// planner rowsplit, rowsplit_fused, xreg, rowphase, rowphase_fused or gemm; prints one line per query with the
 // plan's form ("none" when the planner declines), so tests can check which form a GPU test case
 // reaches on a given CU count.
 int query() {
@@ -199,13 +212,13 @@ int query() {
     } else if (k == "xreg") {
       RowSplitPlan p{};
       std::printf(rowsplit_xreg_plan(M, N, K, cus, &p) ? "xreg blocks=%d\n" : "none\n", p.blocks);
-    } else if (k == "rowphase") {
+    } else if (k == "rowphase" || k == "rowphase_fused") {
       RowPhasePlan p{};
-      if (!rowphase_plan(M, N, K, cus, &p)) {
+      if (!rowphase_plan(M, N, K, cus, &p, k == "rowphase_fused")) {
         std::printf("none\n");
         continue;
       }
-      std::printf("variant=%d S=%d wide=%d blocks=%d\n", p.variant, p.S, (int)p.wide, p.blocks);
+      std::printf("variant=%d S=%d wide=%d blocks=%d BW=%d\n", p.variant, p.S, (int)p.wide, p.blocks, p.BW);
     } else if (k == "gemm") {
       const uint16_t* s = reinterpret_cast<const uint16_t*>(uintptr_t{0x100000});
       const uint16_t* b = reinterpret_cast<const uint16_t*>(uintptr_t{0x200000});

@@ -21,9 +21,13 @@ Row-phase variants of wide plans (qmm4_affine_bf16 at 17-64 rows over N >= 32768
 variant whose waves without a block in the last slot skip that slot's arithmetic (9 or 17 blocks
 per workgroup leave most waves a block short); "full" computes every slot in every wave.
 Routes of the gate+up SiLU·mul projection (qmm4_gate_up_silu_bf16):
-  "fused"     one row-split launch with the epilogue fused;
-  "two-pass"  the projection into the library's scratch, then the SiLU·mul pass (no fused
-              row-split plan: more than 16 rows, or an x slice too large for LDS).
+  "fused"            one row-split launch with the epilogue fused;
+  "row-phase fused"  otherwise, from 5 to 96 rows where the projection takes a wide row-phase plan
+                     (K % 512 == 0; no unfused row-split plan up to 16 rows; at most one range per
+                     CU past 64 rows; ranges no larger than the projection's, or 17 rows or more
+                     with M x K <= 2^19): one row-phase launch whose ranges hold the same blocks
+                     of the gate and up halves, epilogue fused;
+  "two-pass"         the projection into the library's scratch, then the SiLU·mul pass.
 """
 
 CUS = 256
@@ -62,6 +66,15 @@ GATE_UP_CASES = [
     (1, 81920, 32, "two-pass"),   # x slices too large for LDS at every K split
     (3, 81920, 256, "two-pass"),
     (16, 20480, 1024, "two-pass"),
+    (24, 5120, 34816, "row-phase fused"),   # 218 ranges of 5 + 5 blocks, the twin variant
+    (48, 2048, 33024, "row-phase fused"),   # 1032 blocks per half: a partial last range
+    (64, 4096, 32768, "row-phase fused"),   # one block per wave
+    (80, 5120, 34816, "row-phase fused"),   # 80-row x blocks
+    (96, 2048, 34816, "row-phase fused"),
+    (17, 2048, 65536, "row-phase fused"),
+    (12, 20480, 34816, "two-pass"),  # ranges of 10 blocks against the projection's 9, under 17 rows
+    (64, 16384, 34816, "two-pass"),  # ranges of 10 against 9, M x K past 2^19
+    (24, 16384, 32768, "row-phase fused"),  # long K, ranges of 8 blocks as the projection's
     (64, 5120, 1024, "two-pass"),  # row-phase underneath
     (100, 512, 4096, "two-pass"),  # row-phase underneath (112-row x blocks)
     (136, 512, 4096, "two-pass"),  # GEMM underneath

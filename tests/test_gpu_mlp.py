@@ -64,7 +64,9 @@ def check_gate_up(x, w, s, b):
 # partial range, K = 4096 gives units of 4 super-steps, 5120 of 5, 9 to 16 rows take 16-row
 # fragments with K in slices), or the projection into the library's scratch buffer followed by the
 # epilogue pass (x slices too large for LDS at up to 16 rows; the row-phase and GEMM kernels
-# underneath at 64 and 100 rows). tests/test_plans.py checks each case's route against the planner.
+# underneath at 64 and 100 rows), or one row-phase launch with the epilogue fused (5-96 rows over
+# N that gives every CU its own blocks; 33024 leaves the last range 2 + 2 blocks).
+# tests/test_plans.py checks each case's route against the planner.
 @pytest.mark.parametrize("m,k,n,route", GATE_UP_CASES)
 def test_gate_up_silu(m, k, n, route):
     print(f"  gate_up M={m} K={k} N={n} ({route})", flush=True)

@@ -75,13 +75,31 @@ def test_fold_cases_take_their_routes(planner_exe):
 
 
 def test_gate_up_cases_take_their_routes(planner_exe):
-    """Each shape of test_gpu_mlp.py reaches its route on 256 CUs: the fused row-split launch when
-    rowsplit_plan(fused) accepts it (dispatch_gate_up_silu), else the two-pass path."""
+    """Each shape of test_gpu_mlp.py reaches its route on 256 CUs (dispatch_gate_up_silu): the fused
+    row-split launch when rowsplit_plan(fused) accepts it; else, at 5-96 rows with K % 512 == 0 and
+    no unfused row-split plan up to 16 rows, the fused row-phase launch when rowphase_plan(fused)
+    accepts it (at most one range per CU past 64 rows) with ranges no larger than the projection's,
+    or from 17 rows with M x K up to kFusedRowPhaseMaxMK; else the two-pass path."""
+    MAX_MK = 1 << 19
     from route_cases import CUS, GATE_UP_CASES
 
+    nc = len(GATE_UP_CASES)
     lines = [f"rowsplit_fused {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
-    for (m, k, n, route), p in zip(GATE_UP_CASES, query(planner_exe, lines)):
-        assert route == ("two-pass" if p == "none" else "fused"), (m, k, n, route, p)
+    lines += [f"rowphase_fused {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
+    lines += [f"rowsplit {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
+    lines += [f"rowphase {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
+    out = query(planner_exe, lines)
+    for (m, k, n, route), rs, rp, rsp, ru in zip(GATE_UP_CASES, out, out[nc:], out[2 * nc:], out[3 * nc:]):
+        if rs != "none":
+            want = "fused"
+        elif (5 <= m <= 96 and k % 512 == 0 and isinstance(rp, dict) and not (m <= 16 and rsp != "none")
+              and (m <= 64 or int(rp["blocks"]) <= CUS)
+              and (int(rp["BW"]) <= int(ru["BW"]) or (m >= 17 and m * k <= MAX_MK))):
+            assert rp["wide"] == "1" and rp["S"] == "1", (m, k, n, rp)
+            want = "row-phase fused"
+        else:
+            want = "two-pass"
+        assert route == want, (m, k, n, route, rs, rp)
 
 
 def test_mid_row_cases_take_their_routes(planner_exe):
