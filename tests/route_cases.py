@@ -80,6 +80,14 @@ GATE_UP_CASES = [
     (136, 512, 4096, "two-pass"),  # GEMM underneath
 ]
 
+# Seeded random (M, K, N) shapes (M 1-96, N a multiple of 32), reaching all three routes: one row-split launch
+# (fused), one row-phase launch over a wide N (row-phase fused), and the two passes.
+RANDOM_GATE_UP = [(8, 2560, 33056), (11, 512, 35488), (59, 2048, 35136), (89, 2048, 2272), (29, 512, 33568),
+                  (9, 4096, 32768), (29, 2048, 33728), (5, 4608, 3232), (37, 1024, 11040), (64, 2048, 34080),
+                  (23, 1024, 2912), (86, 384, 10656), (6, 512, 33504), (29, 1536, 33664), (32, 4096, 33024),
+                  (60, 3072, 11712), (77, 512, 35040), (3, 1024, 34272), (7, 1024, 6784), (82, 1024, 33952),
+                  (19, 2560, 36512), (34, 2048, 10144), (22, 4096, 36608), (91, 4608, 1728)]
+
 # (M, N, K, route)
 MID_ROW_CASES = [
     (65, 17408, 5120, "row-phase"),   # up projection, one row past 64 (80-row x blocks)

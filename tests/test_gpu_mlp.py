@@ -14,7 +14,7 @@ import torch
 from mlx_tree_spec_amd import STATS, QuantizedLinear, QuantizedMLP, gate_up_silu, quantized_matmul
 from oracle import cpu
 from oracle import qmm4_oracle as O
-from route_cases import GATE_UP_CASES
+from route_cases import GATE_UP_CASES, RANDOM_GATE_UP
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda:0"
@@ -71,6 +71,13 @@ def check_gate_up(x, w, s, b):
 def test_gate_up_silu(m, k, n, route):
     print(f"  gate_up M={m} K={k} N={n} ({route})", flush=True)
     x, w, s, b = O.make_inputs(m, k, n, seed=m + 31 * k + n)
+    check_gate_up(x, w, s, b)
+
+
+@pytest.mark.parametrize("m,k,n", RANDOM_GATE_UP)
+def test_gate_up_silu_random_shapes(m, k, n):
+    print(f"  gate_up random M={m} K={k} N={n}", flush=True)
+    x, w, s, b = O.make_inputs(m, k, n, seed=m * 7919 + k * 31 + n)
     check_gate_up(x, w, s, b)
 
 

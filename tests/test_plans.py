@@ -80,26 +80,45 @@ def test_gate_up_cases_take_their_routes(planner_exe):
     no unfused row-split plan up to 16 rows, the fused row-phase launch when rowphase_plan(fused)
     accepts it (at most one range per CU past 64 rows) with ranges no larger than the projection's,
     or from 17 rows with M x K up to kFusedRowPhaseMaxMK; else the two-pass path."""
-    MAX_MK = 1 << 19
-    from route_cases import CUS, GATE_UP_CASES
+    from route_cases import GATE_UP_CASES
 
-    nc = len(GATE_UP_CASES)
-    lines = [f"rowsplit_fused {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
-    lines += [f"rowphase_fused {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
-    lines += [f"rowsplit {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
-    lines += [f"rowphase {m} {n} {k} {CUS}" for m, k, n, _ in GATE_UP_CASES]
+    routes = gate_up_routes(planner_exe, [(m, k, n) for m, k, n, _ in GATE_UP_CASES])
+    for (m, k, n, route), want in zip(GATE_UP_CASES, routes):
+        assert route == want, (m, k, n, route, want)
+
+
+def test_random_gate_up_shapes_reach_every_route(planner_exe):
+    """test_gpu_mlp.py's seeded random gate+up shapes reach each of the three routes several times."""
+    from route_cases import RANDOM_GATE_UP
+
+    routes = gate_up_routes(planner_exe, RANDOM_GATE_UP)
+    for r in ("fused", "row-phase fused", "two-pass"):
+        assert routes.count(r) >= 5, (r, routes)
+
+
+def gate_up_routes(planner_exe, shapes):
+    """dispatch_gate_up_silu's route for each (M, K, N) on 256 CUs, from the planners' answers."""
+    from route_cases import CUS
+
+    MAX_MK = 1 << 19
+    nc = len(shapes)
+    lines = [f"rowsplit_fused {m} {n} {k} {CUS}" for m, k, n in shapes]
+    lines += [f"rowphase_fused {m} {n} {k} {CUS}" for m, k, n in shapes]
+    lines += [f"rowsplit {m} {n} {k} {CUS}" for m, k, n in shapes]
+    lines += [f"rowphase {m} {n} {k} {CUS}" for m, k, n in shapes]
     out = query(planner_exe, lines)
-    for (m, k, n, route), rs, rp, rsp, ru in zip(GATE_UP_CASES, out, out[nc:], out[2 * nc:], out[3 * nc:]):
+    routes = []
+    for (m, k, n), rs, rp, rsp, ru in zip(shapes, out, out[nc:], out[2 * nc:], out[3 * nc:]):
         if rs != "none":
-            want = "fused"
+            routes.append("fused")
         elif (5 <= m <= 96 and k % 512 == 0 and isinstance(rp, dict) and not (m <= 16 and rsp != "none")
               and (m <= 64 or int(rp["blocks"]) <= CUS)
               and (int(rp["BW"]) <= int(ru["BW"]) or (m >= 17 and m * k <= MAX_MK))):
             assert rp["wide"] == "1" and rp["S"] == "1", (m, k, n, rp)
-            want = "row-phase fused"
+            routes.append("row-phase fused")
         else:
-            want = "two-pass"
-        assert route == want, (m, k, n, route, rs, rp)
+            routes.append("two-pass")
+    return routes
 
 
 def test_mid_row_cases_take_their_routes(planner_exe):
