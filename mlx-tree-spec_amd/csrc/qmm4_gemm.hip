@@ -857,8 +857,15 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   // 10240 244.5 -> 196.3 us; slower with fewer units per workgroup (256 x 8192 -> 5120 44.0 -> 59.6
   // us, 256 x 12288 -> 6144 64.0 -> 68.7 us), at K = 5120 (the up projection at 256-4096 rows,
   // 2-13% slower) and with whole tiles for most CUs (2560 / 3072 x 17408 -> 5120, 200 / 240 tiles:
-  // 413.9 / 446.0 -> 417.3 / 490.2 us; 2048 rows, 160 tiles: 358.9 -> 340.8 us).
-  if (M >= 256 && K >= 8192 && 10 * tiles256 <= 7LL * c && scale_rows_16b(s, b, K) &&
+  // 413.9 / 446.0 -> 417.3 / 490.2 us; 2048 rows, 160 tiles: 358.9 -> 340.8 us). Between 256 and
+  // 512 rows not when the last row of 256-row tiles is at most half full (a quarter to a third of
+  // the MFMA work padding): stream-K over 128 x 256 tiles (below) is faster there, 320 / 384 x
+  // 17408 -> 5120 105.4 / 107.7 -> 89.4 / 92.6 us, 320 / 384 x 12288 -> 5120 79.7 / 82.9 -> 70.3 /
+  // 73.4 us, but not at 448 rows (111.5 / 85.3 -> 113.0 / 87.5 us) nor past 512 rows (640 / 896 /
+  // 1152 / 1408 x 17408 -> 5120 139.2 / 178.9 / 226.2 / 257.9 us against 143.4 / 186.5 / 239.1 /
+  // 285.3 on 128 x 256 tiles; A/B, interleaved rounds, within the parity tolerance).
+  if (M >= 256 && (M > 512 || M % 256 == 0 || M % 256 > 128) && K >= 8192 && 10 * tiles256 <= 7LL * c &&
+      scale_rows_16b(s, b, K) &&
       2 * tiles256 * (K / 512) >= 7LL * c) {
     const size_t slot256 = (size_t)GemmCfg<256, 256>::kPartF4 * 16 * 2;
     if ((size_t)c * slot256 <= ws_capacity) {

@@ -174,7 +174,8 @@ void check_gemm(int M, int N, int K, int cus) {
       GP(p.part_bytes == (size_t)p.G * tm * tn * 4 * 2);
       GP(p.part_bytes <= cap);
       GP(!(p.sk256 && p.sk_wide));
-      if (p.sk256) GP(K % 512 == 0 && M >= 256 && p.G == cus);  // 8-step units, one workgroup per CU
+      if (p.sk256)  // 8-step units, one workgroup per CU; no half-empty last row of tiles below 512 rows
+        GP(K % 512 == 0 && M >= 256 && (M > 512 || M % 256 == 0 || M % 256 > 128) && p.G == cus);
       if (p.sk_wide) GP(K % 512 == 0 && p.G <= cus);           // 8-step units, one workgroup per CU
     } else if (p.tail_sk) {
       // Whole tiles whose last round (fewer quarters than CUs) runs as stream-K over its quarters.

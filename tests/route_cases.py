@@ -139,6 +139,8 @@ GEMM_STREAM_K_CASES = [
     (200, 784, 5120, "128x128"),     # too few units for the wide tiles
     (256, 17408, 5120, "128x256"),
     (320, 17408, 5120, "128x256"),   # a partial row tile
+    (384, 5120, 17408, "128x256"),   # K >= 8192 at 257-384 rows: a half-empty last row of 256-row tiles
+    (320, 5120, 12288, "128x256"),
     (120, 5120, 17408, "128x256"),   # K >= 8192 at 120 rows
     (136, 10256, 5120, "128x256"),   # partial row and column tiles
     (256, 8192, 4096, "128x256"),    # the one-hot exact-dequant case

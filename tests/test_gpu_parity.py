@@ -241,16 +241,18 @@ def workload_ref(x, w, s, b):
 # Also where whole 256 x 256 tiles would fill under half the CUs: 256 and 320 rows of the up
 # projection (272 and 408 tiles of 128), on 128 x 256 tiles, as are 120 x 17408 -> 5120 (K >= 8192)
 # and 136 x 5120 -> 10256 (partial row and column tiles), and 72 / 96 rows over the 65984-column
-# head, where whole tiles would pad the rows to 256 (route_cases.GEMM_STREAM_K_CASES labels the tile
-# size of each). Long K with fewer whole 256 x 256 tiles than CUs takes
-# stream-K over those: 512 and 1024 rows of the down projection (40 and 80 tiles), 384 x 12288 ->
-# 5120 (a half-empty last row tile), 1000 x 8192 -> 4112 (partial row and column tiles). Whole
+# head, where whole tiles would pad the rows to 256, and 320 / 384 rows at K >= 8192 (a last row of
+# 256-row tiles at most half full: 384 x 12288 -> 5120, 384 x 17408 -> 5120, 320 x 12288 -> 5120)
+# (route_cases.GEMM_STREAM_K_CASES labels the tile size of each). Long K with fewer whole 256 x 256
+# tiles than CUs takes stream-K over those: 512 and 1024 rows of the down projection (40 and 80
+# tiles), 1000 x 8192 -> 4112 (partial row and column tiles). Whole
 # tiles whose last round has fewer quarters than CUs run it as stream-K over the quarters: 1024 x
 # 5120 -> 17408 (272 tiles: 256 whole, 16 in quarters), 4096 x 1024 -> 1040 (80 tiles, a partial
 # column of tiles).
 @pytest.mark.parametrize("m,k,n", [(65, 17536, 5120), (128, 5120, 17408), (100, 1152, 4096), (200, 5120, 784),
                                    (96, 640, 1024), (256, 5120, 17408), (320, 5120, 17408),
-                                   (1024, 17408, 5120), (512, 17408, 5120), (384, 12288, 5120),
+                                   (1024, 17408, 5120), (512, 17408, 5120), (384, 12288, 5120), (384, 17408, 5120),
+                                   (320, 12288, 5120),
                                    (1000, 8192, 4112), (1024, 5120, 17408), (4096, 1024, 1040),
                                    (120, 17408, 5120), (136, 5120, 10256), (72, 2048, 65984), (96, 5120, 65984)])
 def test_gemm_stream_k_shapes(m, k, n):
