@@ -883,7 +883,11 @@ bool gemm_plan(int M, int N, int K, int cus, size_t ws_capacity, const uint16_t*
   // MI355X (A/B, interleaved rounds): 192 / 256 / 384 x 5120 -> 17408 85.7 / 89.6 / 118.4 -> 71.5
   // / 73.4 / 109.4 us (68 or 136 whole tiles), 1024 x 17408 -> 5120 278.3 -> 251.4 us (80 whole
   // tiles); 1536 x 17408 -> 5120 (120 full whole tiles, 480 quarters) 316 us, 419 on stream-K;
-  // 512 and 1024 x 5120 -> 17408 (136 and 272 full tiles) stay on whole tiles.
+  // 512 and 1024 x 5120 -> 17408 (136 and 272 full tiles) stay on whole tiles. Stream-K (over
+  // 128 x 256 tiles) wherever whole tiles fill less than one round was slower on the role-split
+  // whole tiles: 640 / 768 x 5120 -> 17408 (204 tiles) 129.1 / 135.8 -> 146.9 / 168.2 us, 1536 /
+  // 2048 x 5120 -> 5120 99.9 / 121.5 -> 109.8 / 133.7 us, 512 x 5120 -> 17408 118.9 -> 120.0 us;
+  // 2-4% faster only at 96 tiles (512 x 5120 -> 12288, 1024 x 5120 -> 6144).
   const long long tiles = (long long)((M + 127) / 128) * ((N + 127) / 128);
   const bool sk_tiles = tiles <= c || (2 * tiles256 < c && 4 * tiles <= 5LL * c) ||
                         (M % 256 != 0 && tiles256 < c && tiles <= 2LL * c);
