@@ -643,7 +643,8 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan, bool fused)
   // shorter walk (blocks x phases of its K slice x super-steps per phase) with the grid filling
   // the CUs; a tie keeps the smaller ranges (fewer partial tiles to add). 17-32 rows over
   // 5120 -> 17408: 68 ranges x 3 slices (204 workgroups) took 31.0-32.0 us, 46 x 5 (230)
-  // 28.1-28.7 us; 17408 -> 5120 ties and keeps 20 x 12. Ranges of one block per wave (twice the
+  // 28.1-28.7 us; 17408 -> 5120 ties and keeps 20 x 12 (14 x 18 of 3 blocks per wave: 16 / 48 /
+  // 64 rows 22.6 / 30.9 / 32.3 -> 24.2 / 34.3 / 35.6 us). Ranges of one block per wave (twice the
   // ranges, half the K slices, the same walk) when those ranges would leave a workgroup at most
   // 3 phases, too few to pipeline: 32 / 64 x 5120 -> 5120 17.0 / 20.6 -> 16.0 / 19.4 us,
   // 16 / 32 x 17408 -> 5120 24.8 / 27.9 -> 22.6 / 26.5 us; with 6 phases (64 x 17408 -> 5120)
