@@ -73,6 +73,7 @@ GATE_UP_CASES = [
     (96, 2048, 34816, "row-phase fused"),
     (17, 2048, 65536, "row-phase fused"),
     (12, 20480, 34816, "two-pass"),  # ranges of 10 blocks against the projection's 9, under 17 rows
+    (12, 20480, 32768, "row-phase fused"),  # 5-16 rows with no row-split plan, ranges of 8 in both
     (64, 16384, 34816, "two-pass"),  # ranges of 10 against 9, M x K past 2^19
     (24, 16384, 32768, "row-phase fused"),  # long K, ranges of 8 blocks as the projection's
     (64, 5120, 1024, "two-pass"),  # row-phase underneath
