@@ -47,6 +47,9 @@ FOLD_CASES = [
     (5, 5120, 5120, False, "two launches"),  # 5 rows: norm kernel + row-split (8-row fragments)
     (4, 5120, 10240, False, "two launches"),  # K > 8192
     (16, 8192, 1024, True, "two launches"),  # 16 rows: norm kernel + fused gate+up (K in 2 slices)
+    (24, 34816, 5120, True, "two launches"),   # norm kernel + the fused row-phase gate+up
+    (48, 33024, 2048, True, "two launches"),
+    (64, 17408, 5120, False, "two launches"),  # norm kernel + row-phase (K split)
 ]
 
 # (M, K, N, route): gate+up weights [N, K] stacked as [gate; up].

@@ -12,7 +12,8 @@ qmm4_add_rms_norm_qmm_bf16 replaces the pair add_rms_norm + projection of tree_v
 The shapes (route_cases.FOLD_CASES, whose routes tests/test_plans.py checks against the planner)
 cover each form of the folded kernel (whole K, K in 2 slices for the plain and the gate+up
 epilogue, units of 4 and 5 super-steps, K from 512 to the largest folded 8192) and the shapes that
-run as two launches (5 rows, K > 8192, 16 rows).
+run as two launches (5 rows, K > 8192, 16 rows, and 24-64 rows over the row-phase kernel, fused
+gate+up or K split).
 """
 
 import numpy as np
