@@ -343,21 +343,34 @@ int dispatch_gate_up_silu(DeviceInfo* di, const void* x, const uint32_t* w, cons
     if (e != hipSuccess) return hip_error(e, "fused gate+up row-split kernel launch");
     return QMM4_OK;
   }
-  // Rows the projection would give a wide row-phase plan (not the row-split kernel, up to 16 rows):
-  // that plan with the epilogue fused, each range holding the same blocks of the gate and up
-  // halves. Against the projection and the epilogue pass (A/B, 5120 -> 34816): 24 / 32 / 48 / 64 /
-  // 80 / 96 rows 40.8 / 42.6 / 52.6 / 59.0 / 66.8 / 73.3 us against 42.6 / 44.0 / 54.2 / 60.6 /
-  // 67.7 / 74.5 us, the same bits; 24 x 16384 -> 32768 (ranges of 8 blocks in both) 84.9 against
-  // 89.1 us.
+  // Rows the projection would give the row-phase kernel (not the row-split kernel, up to 16 rows):
+  // its plan with the epilogue fused, each range holding the same blocks of the gate and up
+  // halves. Wide plans (every workgroup its own blocks over all of K) apply it in the kernel's
+  // epilogue. Against the projection and the epilogue pass (A/B, 5120 -> 34816): 24 / 32 / 48 /
+  // 64 / 80 / 96 rows 40.8 / 42.6 / 52.6 / 59.0 / 66.8 / 73.3 us against 42.6 / 44.0 / 54.2 /
+  // 60.6 / 67.7 / 74.5 us, the same bits; 24 x 16384 -> 32768 (ranges of 8 blocks in both) 84.9
+  // against 89.1 us. Narrow plans (K split over the CUs) are the projection's own, the epilogue in
+  // their reduce kernel.
   if (M >= 5 && M <= kRowPhaseMaxMWide && aligned(scales, 16) && aligned(biases, 16) && K % 512 == 0 &&
-      !(M <= 16 && rowsplit_plan((int)M, (int)N, (int)K, di->cus, false, &rplan))) {
+      !(M <= 16 && (rowsplit_plan((int)M, (int)N, (int)K, di->cus, false, &rplan) ||
+                    (M >= 9 && rowsplit_xreg_plan((int)M, (int)N, (int)K, di->cus, &rplan))))) {
     RowPhasePlan pplan, uplan;
-    if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan, true) && (M <= 64 || pplan.ranges <= di->cus) &&
-        rowphase_plan((int)M, (int)N, (int)K, di->cus, &uplan) &&
-        (pplan.BW <= uplan.BW || (M >= 17 && M * K <= kFusedRowPhaseMaxMK))) {
-      e = launch_rowphase(pplan, xb, w, sb, bb, yb, nullptr, (int)M, (int)N, (int)K, stream);
-      if (e != hipSuccess) return hip_error(e, "fused gate+up row-phase kernel launch");
-      return QMM4_OK;
+    if (rowphase_plan((int)M, (int)N, (int)K, di->cus, &pplan, true) &&
+        rowphase_plan((int)M, (int)N, (int)K, di->cus, &uplan)) {
+      const bool take = pplan.wide ? (M <= 64 || pplan.ranges <= di->cus) &&
+                                         (pplan.BW <= uplan.BW || (M >= 17 && M * K <= kFusedRowPhaseMaxMK))
+                                   : M >= 17 || 2 * pplan.blocks >= di->cus;
+      if (take) {
+        uint32_t* pcnt = nullptr;
+        float* ppart = nullptr;
+        if (pplan.S > 1) {
+          rc = ws.get(0, pplan.part_bytes, &pcnt, &ppart);
+          if (rc) return rc;
+        }
+        e = launch_rowphase(pplan, xb, w, sb, bb, yb, ppart, (int)M, (int)N, (int)K, stream);
+        if (e != hipSuccess) return hip_error(e, "fused gate+up row-phase kernel launch");
+        return QMM4_OK;
+      }
     }
   }
   // Otherwise the projection into a library-held [M, N] buffer, then the epilogue as its own pass.

@@ -465,7 +465,7 @@ constexpr int kRedThreads = 256;
 template <class C>
 __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhaseParams P) {
   constexpr int MB = C::MB, BPW = C::BPW, kRpWaves = C::kRpWaves;
-  const int ranges = (P.NB + P.BW - 1) / P.BW;
+  const int ranges = P.ranges;
   const int it = blockIdx.x * kRedThreads + threadIdx.x;
   const int range = it / C::kItems;
   if (range >= ranges) return;
@@ -475,38 +475,64 @@ __global__ __launch_bounds__(kRedThreads) void rowphase_reduce_kernel(RowPhasePa
   const int ii = rest % MB, wj = rest / MB;
   const int j = wj % BPW, wave = wj / BPW;
   const int blk = wave + kRpWaves * j;  // block within the range
-  const int b0 = range * P.BW;
-  if (blk >= min(P.BW, P.NB - b0)) return;  // no such block: the first pass stored nothing
   const int n = lane & 15, g = lane >> 4;
-  const int col = (b0 + blk) * 16 + n;
+  // Fused gate+up: the range's gate blocks are its local blocks 0 .. hb - 1 and their up blocks
+  // hb .. 2 hb - 1; a gate item's thread also adds its up item and writes silu(gate) * up.
+  const bool fused = C::kFusable && P.fused;
+  const int hb0 = range * (P.BW >> 1);
+  const int hb = fused ? min(P.BW >> 1, (P.NB >> 1) - hb0) : 0;
+  const int b0 = range * P.BW;
+  if (fused ? blk >= hb : blk >= min(P.BW, P.NB - b0)) return;  // no such block (or an up block)
+  const int col = fused ? (hb0 + blk) * 16 + n : (b0 + blk) * 16 + n;
+  const int ublk = blk + hb;
+  const int uitem = ((((ublk % kRpWaves) * BPW + ublk / kRpWaves) * MB + ii) << 6) + lane;
   const __amdgpu_buffer_rsrc_t rp = __builtin_amdgcn_make_buffer_rsrc(
       P.part, 0, rsrc_bytes((unsigned long long)ranges * P.S * C::kItems * 16), kBufferRsrcWord3);
-  f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
   const uint32_t base = (uint32_t)range * (uint32_t)P.S;
-  // kRedBatch contributors' loads in flight at a time (one memory round trip for the usual S of
-  // 10-12); past the last they read zero (an offset outside the buffer), and adding +0 leaves a
-  // sum that is not -0 unchanged (a sum from +0 never is -0).
+  // The S partial tiles' item `itm` added in workgroup order. kRedBatch contributors' loads in
+  // flight at a time (one memory round trip for the usual S of 10-12); past the last they read
+  // zero (an offset outside the buffer), and adding +0 leaves a sum that is not -0 unchanged (a
+  // sum from +0 never is -0).
   constexpr int kRedBatch = 16;
-  for (int q = 0; q < P.S; q += kRedBatch) {
-    f32x4 v[kRedBatch];
+  auto add_slices = [&](int itm) __attribute__((always_inline)) {
+    f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+    for (int q = 0; q < P.S; q += kRedBatch) {
+      f32x4 v[kRedBatch];
 #pragma unroll
-    for (int u = 0; u < kRedBatch; ++u) {
-      const uint32_t off = q + u < P.S ? ((base + (uint32_t)(q + u)) * C::kItems + (uint32_t)item) * 16u : 0x80000000u;
-      v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kCoherent));
-    }
+      for (int u = 0; u < kRedBatch; ++u) {
+        const uint32_t off =
+            q + u < P.S ? ((base + (uint32_t)(q + u)) * C::kItems + (uint32_t)itm) * 16u : 0x80000000u;
+        v[u] = __builtin_bit_cast(f32x4, __builtin_amdgcn_raw_buffer_load_b128(rp, off, 0, kCoherent));
+      }
 #pragma unroll
-    for (int u = 0; u < kRedBatch; ++u) {
-      sum[0] += v[u][0]; sum[1] += v[u][1]; sum[2] += v[u][2]; sum[3] += v[u][3];
+      for (int u = 0; u < kRedBatch; ++u) {
+        sum[0] += v[u][0]; sum[1] += v[u][1]; sum[2] += v[u][2]; sum[3] += v[u][3];
+      }
     }
-  }
+    return sum;
+  };
+  const f32x4 sum = add_slices(item);
+  const int ny = fused ? P.N >> 1 : P.N;  // columns of y
   const __amdgpu_buffer_rsrc_t ry = __builtin_amdgcn_make_buffer_rsrc(
-      P.y, 0, rsrc_bytes((unsigned long long)P.M * P.N * 2), kBufferRsrcWord3);
+      P.y, 0, rsrc_bytes((unsigned long long)P.M * ny * 2), kBufferRsrcWord3);
+  if (fused) {
+    const f32x4 up = add_slices(uitem);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int m = ii * 16 + 4 * g + r;
+      if (m < P.M)
+        __builtin_amdgcn_raw_buffer_store_b16(
+            (uint16_t)silu_mul_bf16(pack_bf16x2(sum[r], 0.0f) & 0xFFFFu, pack_bf16x2(up[r], 0.0f) & 0xFFFFu), ry,
+            ((uint32_t)m * (uint32_t)ny + (uint32_t)col) * 2u, 0, 0);
+    }
+    return;
+  }
 #pragma unroll
   for (int r = 0; r < 4; ++r) {
     const int m = ii * 16 + 4 * g + r;
     if (m < P.M)
       __builtin_amdgcn_raw_buffer_store_b16((uint16_t)(pack_bf16x2(sum[r], 0.0f) & 0xFFFFu), ry,
-                                            ((uint32_t)m * (uint32_t)P.N + (uint32_t)col) * 2u, 0, 0);
+                                            ((uint32_t)m * (uint32_t)ny + (uint32_t)col) * 2u, 0, 0);
   }
 }
 
@@ -592,9 +618,11 @@ bool rowphase_plan(int M, int N, int K, int cus, RowPhasePlan* plan, bool fused)
   // kRpNarrowBpw blocks per wave, K split over the CUs.
   constexpr int kW = 8;  // waves per workgroup of every variant
   const bool wide = NB >= kW * cus;
-  // Fused gate+up (N = 2 n stacked rows): wide plans only, each range the same BW / 2 blocks of
-  // both halves, so that the SiLU·mul epilogue finds gate and up columns in one tile.
-  if (fused && (!wide || M > 96)) return false;
+  // Fused gate+up (N = 2 n stacked rows): each range the same BW / 2 blocks of both halves, so that
+  // the SiLU·mul epilogue finds gate and up columns in one tile (the first pass's, or with K split
+  // the reduce kernel's). Narrow plans keep the projection's: ceil(NB / BW) = ceil(NB / 2 / (BW / 2))
+  // ranges either way, so the same K slices and the same bits.
+  if (fused && M > 96) return false;
   const int NBh = NB / 2;
   // The variant for mb rows with the fewest blocks per wave that still holds `want` (or the most).
   auto pick = [&](int want) {
@@ -737,8 +765,7 @@ hipError_t launch_rowphase(const RowPhasePlan& plan, const uint16_t* x, const ui
   if (plan.fused) {
     int cm, cv, cb, items;
     size_t l;
-    if (!rowphase_geometry(plan.variant, &cm, &cv, &cb, &l, &items) || cm > 6 || plan.S != 1 || plan.BW % 2 != 0 ||
-        N % 32 != 0)
+    if (!rowphase_geometry(plan.variant, &cm, &cv, &cb, &l, &items) || cm > 6 || plan.BW % 2 != 0 || N % 32 != 0)
       return hipErrorInvalidValue;
   }
   const void* f = rowphase_func(plan.variant);

@@ -130,10 +130,16 @@ void check_rowphase(int M, int N, int K, int cus) {
   const char* ff = "rowphase fused M=%d N=%d K=%d cus=%d";
 #define RF(cond) CHECK(cond, ff, M, N, K, cus)
   const int nbh = N / 32;
-  RF(q.fused && q.wide && q.S == 1 && q.part_bytes == 0);
+  RF(q.fused && M <= 96 && q.wide == p.wide);
   RF(q.BW >= 2 && q.BW % 2 == 0);
   RF((long long)q.ranges * (q.BW / 2) >= nbh && (long long)(q.ranges - 1) * (q.BW / 2) < nbh);
-  RF(q.blocks == q.ranges && q.lds <= kLds && q.NP >= 1);
+  RF(q.blocks == q.ranges * q.S && q.lds <= kLds && q.NP >= 1);
+  if (q.wide) {
+    RF(q.S == 1 && q.part_bytes == 0);
+  } else {  // the projection's own plan (the same K slices: the same bits)
+    RF(q.variant == p.variant && q.BW == p.BW && q.S == p.S && q.NP == p.NP && q.ranges == p.ranges &&
+       q.part_bytes == p.part_bytes);
+  }
 #undef RF
 }
 

@@ -22,11 +22,12 @@ variant whose waves without a block in the last slot skip that slot's arithmetic
 per workgroup leave most waves a block short); "full" computes every slot in every wave.
 Routes of the gate+up SiLU·mul projection (qmm4_gate_up_silu_bf16):
   "fused"            one row-split launch with the epilogue fused;
-  "row-phase fused"  otherwise, from 5 to 96 rows where the projection takes a wide row-phase plan
-                     (K % 512 == 0; no unfused row-split plan up to 16 rows; at most one range per
-                     CU past 64 rows; ranges no larger than the projection's, or 17 rows or more
-                     with M x K <= 2^19): one row-phase launch whose ranges hold the same blocks
-                     of the gate and up halves, epilogue fused;
+  "row-phase fused"  otherwise, from 5 to 96 rows where the projection takes the row-phase kernel
+                     (K % 512 == 0; no row-split plan up to 16 rows): its ranges hold the same
+                     blocks of the gate and up halves and the epilogue is fused, in the kernel for
+                     a wide plan (at most one range per CU past 64 rows; ranges no larger than the
+                     projection's, or 17 rows or more with M x K <= 2^19), in the reduce kernel for
+                     the projection's own K-split plan;
   "two-pass"         the projection into the library's scratch, then the SiLU·mul pass.
 """
 
@@ -68,7 +69,7 @@ GATE_UP_CASES = [
     (16, 1024, 2048, "fused"),
     (1, 81920, 32, "two-pass"),   # x slices too large for LDS at every K split
     (3, 81920, 256, "two-pass"),
-    (16, 20480, 1024, "two-pass"),
+    (16, 20480, 1024, "row-phase fused"),  # the projection's K-split plan, the epilogue in its reduce
     (24, 5120, 34816, "row-phase fused"),   # 218 ranges of 5 + 5 blocks, the twin variant
     (48, 2048, 33024, "row-phase fused"),   # 1032 blocks per half: a partial last range
     (64, 4096, 32768, "row-phase fused"),   # one block per wave
@@ -79,18 +80,21 @@ GATE_UP_CASES = [
     (12, 20480, 32768, "row-phase fused"),  # 5-16 rows with no row-split plan, ranges of 8 in both
     (64, 16384, 34816, "two-pass"),  # ranges of 10 against 9, M x K past 2^19
     (24, 16384, 32768, "row-phase fused"),  # long K, ranges of 8 blocks as the projection's
-    (64, 5120, 1024, "two-pass"),  # row-phase underneath
+    (64, 5120, 1024, "row-phase fused"),  # K split over the CUs: the reduce kernel applies the epilogue
     (100, 512, 4096, "two-pass"),  # row-phase underneath (112-row x blocks)
     (136, 512, 4096, "two-pass"),  # GEMM underneath
 ]
 
-# Seeded random (M, K, N) shapes (M 1-96, N a multiple of 32), reaching all three routes: one row-split launch
-# (fused), one row-phase launch over a wide N (row-phase fused), and the two passes.
+# Seeded random (M, K, N) shapes (M 1-120, N a multiple of 32), reaching all three routes: one row-split
+# launch (fused), the row-phase kernel with the epilogue fused (row-phase fused: wide plans, or the
+# K-split plans' reduce kernel), and the two passes (K % 512 != 0, past 96 rows).
 RANDOM_GATE_UP = [(8, 2560, 33056), (11, 512, 35488), (59, 2048, 35136), (89, 2048, 2272), (29, 512, 33568),
                   (9, 4096, 32768), (29, 2048, 33728), (5, 4608, 3232), (37, 1024, 11040), (64, 2048, 34080),
                   (23, 1024, 2912), (86, 384, 10656), (6, 512, 33504), (29, 1536, 33664), (32, 4096, 33024),
                   (60, 3072, 11712), (77, 512, 35040), (3, 1024, 34272), (7, 1024, 6784), (82, 1024, 33952),
-                  (19, 2560, 36512), (34, 2048, 10144), (22, 4096, 36608), (91, 4608, 1728)]
+                  (19, 2560, 36512), (34, 2048, 10144), (22, 4096, 36608), (91, 4608, 1728),
+                  (40, 640, 8192), (70, 1152, 4096), (100, 2048, 4096), (120, 1024, 8192), (12, 2432, 6144),
+                  (27, 4736, 2048)]
 
 # (M, N, K, route)
 MID_ROW_CASES = [

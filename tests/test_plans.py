@@ -77,9 +77,8 @@ def test_fold_cases_take_their_routes(planner_exe):
 def test_gate_up_cases_take_their_routes(planner_exe):
     """Each shape of test_gpu_mlp.py reaches its route on 256 CUs (dispatch_gate_up_silu): the fused
     row-split launch when rowsplit_plan(fused) accepts it; else, at 5-96 rows with K % 512 == 0 and
-    no unfused row-split plan up to 16 rows, the fused row-phase launch when rowphase_plan(fused)
-    accepts it (at most one range per CU past 64 rows) with ranges no larger than the projection's,
-    or from 17 rows with M x K up to kFusedRowPhaseMaxMK; else the two-pass path."""
+    no unfused row-split plan up to 16 rows, the fused row-phase launch (gate_up_routes); else the
+    two-pass path."""
     from route_cases import GATE_UP_CASES
 
     routes = gate_up_routes(planner_exe, [(m, k, n) for m, k, n, _ in GATE_UP_CASES])
@@ -97,7 +96,11 @@ def test_random_gate_up_shapes_reach_every_route(planner_exe):
 
 
 def gate_up_routes(planner_exe, shapes):
-    """dispatch_gate_up_silu's route for each (M, K, N) on 256 CUs, from the planners' answers."""
+    """dispatch_gate_up_silu's route for each (M, K, N) on 256 CUs, from the planners' answers: the
+    fused row-split launch; else the row-phase plan the projection would take (5-96 rows, K % 512 ==
+    0, no row-split or x-in-registers plan up to 16 rows), fused: a wide plan under the range-size
+    rule, a narrow (K-split) plan where the projection takes it (17 rows or more, or a K split
+    filling half the CUs); else the two passes."""
     from route_cases import CUS
 
     MAX_MK = 1 << 19
@@ -106,18 +109,23 @@ def gate_up_routes(planner_exe, shapes):
     lines += [f"rowphase_fused {m} {n} {k} {CUS}" for m, k, n in shapes]
     lines += [f"rowsplit {m} {n} {k} {CUS}" for m, k, n in shapes]
     lines += [f"rowphase {m} {n} {k} {CUS}" for m, k, n in shapes]
+    lines += [f"xreg {m} {n} {k} {CUS}" for m, k, n in shapes]
     out = query(planner_exe, lines)
     routes = []
-    for (m, k, n), rs, rp, rsp, ru in zip(shapes, out, out[nc:], out[2 * nc:], out[3 * nc:]):
-        if rs != "none":
-            routes.append("fused")
-        elif (5 <= m <= 96 and k % 512 == 0 and isinstance(rp, dict) and not (m <= 16 and rsp != "none")
-              and (m <= 64 or int(rp["blocks"]) <= CUS)
-              and (int(rp["BW"]) <= int(ru["BW"]) or (m >= 17 and m * k <= MAX_MK))):
-            assert rp["wide"] == "1" and rp["S"] == "1", (m, k, n, rp)
-            routes.append("row-phase fused")
-        else:
-            routes.append("two-pass")
+    for i, (m, k, n) in enumerate(shapes):
+        rs, rp, rsp, ru, xr = out[i], out[nc + i], out[2 * nc + i], out[3 * nc + i], out[4 * nc + i]
+        take = False
+        if (rs == "none" and 5 <= m <= 96 and k % 512 == 0 and isinstance(rp, dict) and isinstance(ru, dict)
+                and not (m <= 16 and (rsp != "none" or (m >= 9 and xr != "none")))):
+            if rp["wide"] == "1":
+                assert rp["S"] == "1", (m, k, n, rp)
+                take = ((m <= 64 or int(rp["blocks"]) <= CUS)
+                        and (int(rp["BW"]) <= int(ru["BW"]) or (m >= 17 and m * k <= MAX_MK)))
+            else:  # the projection's own K-split plan
+                assert {key: rp[key] for key in ("variant", "S", "BW", "blocks")} == \
+                    {key: ru[key] for key in ("variant", "S", "BW", "blocks")}, (m, k, n, rp, ru)
+                take = m >= 17 or 2 * int(rp["blocks"]) >= CUS
+        routes.append("fused" if rs != "none" else "row-phase fused" if take else "two-pass")
     return routes
 
 
