@@ -199,19 +199,20 @@ def time_graph(torch, call, reps: int = 20, replays: int = 5) -> float:
 
 def measure_fused(torch, lib, dev, wl: Workload) -> dict:
     """The ops either side of the projection: the fused gate+up with its SiLU·mul epilogue on the c1
-    weights (the gate and up projections stacked; decode rows and a 16-row verify batch), and the
+    weights (the gate and up projections stacked; decode rows, and 16- and 64-row verify batches:
+    the row-split kernel's and the row-phase kernel's fused forms), and the
     residual add + RMS norm at the model
     width for decode (4 rows) and a prefill chunk (4096 rows). Timed as graph replays of 20
     back-to-back calls on rotating inputs (no host dispatch in the figure). HBM-bound; bytes are the
     algorithmic ones (weights, scales and biases, x, y; for the norm x, r, h, n and the weight row)."""
     out = {}
     n2 = wl.n // 2
-    # Decode rows on the workload's x, and a 16-row tree-verify batch.
+    # Decode rows on the workload's x, and 16- and 64-row tree-verify batches.
     g16 = torch.Generator(device="cpu").manual_seed(16)
-    x16 = torch.randn(16, wl.k, generator=g16).to(torch.bfloat16).to(dev)
-    for m in (*wl.rows, 16):
+    xv = {r: torch.randn(r, wl.k, generator=g16).to(torch.bfloat16).to(dev) for r in (16, 64)}
+    for m in (*wl.rows, 16, 64):
         y = torch.empty((m, n2), dtype=torch.int16, device=dev)
-        xm = wl.x if m <= max(wl.rows) else x16
+        xm = wl.x if m <= max(wl.rows) else xv[m]
 
         def call(i, stream, m=m, y=y, xm=xm):
             c = i % wl.copies
